@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X skinny decode GEMM (one GPU).
+
+Headline (one JSON line on stdout): the BASELINE C4 workload — a full
+Qwen3-4B decode-step GEMM sweep at M = 32: 36 layers x {qkv 2560->6144,
+o 4096->2560, gate_up 2560->19456 + SiLU*mul, down 9728->2560} + lm_head
+2560->151936, every layer with its own seeded bf16 weights (8.04 GB, far past
+the 256 MB Infinity Cache).  A step is one sweep (145 GEMM calls) replayed from
+a HIP graph; ``value`` is algorithmic HBM bytes per second over K steps.
+
+Also reported: the per-GEMM table of the metric (µs, GB/s, % of 8 TB/s at
+M = 1, 8, 64 for every projection, torch F.linear on the GPU timed the same
+way), the roofline of the dominant kernel, and the CPU baseline (torch bf16
+F.linear on this host's cores, the reference's own call).
+
+Algorithmic bytes per call: 2·(N_w·K + M·K + M·N_out).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "kernel-rush-kawk_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+HIDDEN, INTER, VOCAB, LAYERS, QW = 2560, 9728, 151936, 36, 4096
+# name -> (K, N_w, silu)
+SHAPES = {
+    "qkv": (HIDDEN, 6144, False),
+    "o": (QW, HIDDEN, False),
+    "gate_up": (HIDDEN, 2 * INTER, True),
+    "down": (INTER, HIDDEN, False),
+    "lm_head": (HIDDEN, VOCAB, False),
+}
+TENSOR_ID = {"x": 0, "qkv": 1, "o": 2, "gate_up": 3, "down": 4, "lm_head": 5}
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def algo_bytes(name: str, M: int) -> int:
+    K, Nw, silu = SHAPES[name]
+    nout = Nw // 2 if silu else Nw
+    return 2 * (Nw * K + M * K + M * nout)
+
+
+def seed_for(config: int, layer: int, tensor: str) -> int:
+    return 1000 * config + 10 * layer + TENSOR_ID[tensor]
+
+
+def randn_bf16(torch, shape, seed, scale, device):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    t = torch.randn(shape, generator=g, dtype=torch.float32, device=device)
+    return t.mul_(scale).to(torch.bfloat16)
+
+
+def graph_time_ms(torch, calls, reps: int = 5):
+    """Median over ``reps`` replays of one graph holding ``calls`` (a list of
+    closures), divided by len(calls): milliseconds per call."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls[:3]:
+            c()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    g.replay()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        samples.append(a.elapsed_time(b) / len(calls))
+    samples.sort()
+    return samples[len(samples) // 2], g
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--M", type=int, default=32, help="rows of the headline sweep (C4: 32)")
+    ap.add_argument("--no-table", action="store_true", help="skip the per-GEMM M=1/8/64 table")
+    ap.add_argument("--no-torch", action="store_true", help="skip the torch-GPU comparison timings")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample length")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (collectives are out of "
+              "scope); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    import torch.nn.functional as F
+
+    from kernels import gemm as G
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
+
+    # ------------------------------------------------------------ weights
+    t0 = time.time()
+    cfgid = 4
+    layers = []
+    for l in range(LAYERS):
+        layers.append({name: randn_bf16(torch, (SHAPES[name][1], SHAPES[name][0]), seed_for(cfgid, l, name), 0.02, dev)
+                       for name in ("qkv", "o", "gate_up", "down")})
+    lm = [randn_bf16(torch, (VOCAB, HIDDEN), seed_for(cfgid, 99, "lm_head") + i, 0.02, dev) for i in range(2)]
+    torch.cuda.synchronize()
+    log(f"weights: {sum(t.numel() for L in layers for t in L.values()) * 2 / 1e9 + 2 * lm[0].numel() * 2 / 1e9:.2f} GB "
+        f"in {time.time() - t0:.1f}s")
+
+    # ------------------------------------------------------------ headline sweep
+    M = args.M
+    x = {name: randn_bf16(torch, (M, SHAPES[name][0]), seed_for(cfgid, 0, "x") + SHAPES[name][0], 1.0, dev)
+         for name in ("qkv", "o", "gate_up", "down", "lm_head")}
+    ops = {name: (G.SkinnyGateUp(M, SHAPES[name][1] // 2, SHAPES[name][0], dev) if SHAPES[name][2]
+                  else G.SkinnyMatmul(M, SHAPES[name][1], SHAPES[name][0], dev))
+           for name in SHAPES}
+    outs = {name: torch.empty((M, SHAPES[name][1] // 2 if SHAPES[name][2] else SHAPES[name][1]),
+                              dtype=torch.bfloat16, device=dev) for name in SHAPES}
+
+    def sweep():
+        for L in layers:
+            for name in ("qkv", "o", "gate_up", "down"):
+                ops[name].run(x[name], L[name], outs[name])
+        ops["lm_head"].run(x["lm_head"], lm[0], outs["lm_head"])
+
+    # parity spot check of the sweep's calls against torch on the GPU (not the oracle)
+    sweep()
+    torch.cuda.synchronize()
+    for name in ("qkv", "o", "gate_up", "down"):
+        ref = F.linear(x[name], layers[-1][name])
+        if SHAPES[name][2]:
+            ref = F.silu(ref[:, :INTER]) * ref[:, INTER:]
+        err = (outs[name].float() - ref.float()).abs()
+        tol = 2e-2 + 1e-2 * ref.float().abs()
+        if not bool((err <= tol).all()):
+            log(f"PARITY FAILURE in {name}: max err {err.max().item():.4g}")
+            return 1
+    ref_lm = F.linear(x["lm_head"], lm[0])
+    argmax_ok = bool(torch.equal(ref_lm.argmax(-1), outs["lm_head"].argmax(-1)))
+
+    sweep_bytes = LAYERS * sum(algo_bytes(n, M) for n in ("qkv", "o", "gate_up", "down")) + algo_bytes("lm_head", M)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        sweep()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g_sweep = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_sweep):
+        sweep()
+    for _ in range(args.warmup):
+        g_sweep.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(args.steps):
+        g_sweep.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"sweep M={M}: {ms_per_step * 1000:.1f} us/step, {value:.0f} GB/s ({100 * value / HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+
+    # ------------------------------------------------------------ dominant kernel roofline
+    # gate_up carries 45% of a sweep's bytes.  Its average launch duration is
+    # timed with HIP events on the replay stream around a graph of 36
+    # back-to-back launches over the 36 distinct layer weights.
+    dom = "gate_up"
+    dom_calls = [(lambda L=L: ops[dom].run(x[dom], L[dom], outs[dom])) for L in layers]
+    dom_ms, _ = graph_time_ms(torch, dom_calls, reps=max(5, args.steps // 4))
+    dom_bytes = algo_bytes(dom, M)
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": f"{dom} M={M} (mfma_gemm_kernel SILU)", "us_per_launch": round(dom_ms * 1000, 2),
+                "bytes_per_launch": dom_bytes}
+    log(f"roofline {dom}: {dom_ms * 1000:.2f} us/launch, {achieved:.0f} GB/s")
+
+    # ------------------------------------------------------------ per-GEMM table (M = 1, 8, 64)
+    table = []
+    if not args.no_table:
+        for Mt in (1, 8, 64):
+            for name in SHAPES:
+                K, Nw, silu = SHAPES[name]
+                xt = randn_bf16(torch, (Mt, K), 77 + Mt + K, 1.0, dev)
+                op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
+                ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
+                ws = lm if name == "lm_head" else [L[name] for L in layers]
+                n = 2 * len(ws) if name == "lm_head" else len(ws)
+                calls = [(lambda w=ws[i % len(ws)]: op.run(xt, w, ot)) for i in range(n)]
+                ms, _ = graph_time_ms(torch, calls)
+                row = {"shape": name, "M": Mt, "us": round(ms * 1000, 2),
+                       "GBps": round(algo_bytes(name, Mt) / (ms * 1e-3) / 1e9, 1)}
+                row["pct_peak"] = round(100 * row["GBps"] / HBM_PEAK_GBPS, 1)
+                row["config"] = op.resolved_config
+                if not args.no_torch:
+                    if silu:
+                        tcalls = [(lambda w=ws[i % len(ws)]: (lambda r: F.silu(r[:, :INTER]) * r[:, INTER:])(F.linear(xt, w)))
+                                  for i in range(n)]
+                    else:
+                        tcalls = [(lambda w=ws[i % len(ws)]: F.linear(xt, w)) for i in range(n)]
+                    tms, _ = graph_time_ms(torch, tcalls)
+                    row["torch_gpu_us"] = round(tms * 1000, 2)
+                table.append(row)
+                log(f"M={Mt:3d} {name:8s} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s {row['pct_peak']:5.1f}%"
+                    + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
+
+    # ------------------------------------------------------------ CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, layers[0], lm[0], x, M, args.cpu_seconds)
+
+    result = {
+        "metric": "HBM GB/s (% of peak) & µs per Qwen3-4B decode GEMM at M=1/8/64",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) bf16 weights, random init)",
+        "config": {"workload": f"C4 decode-step GEMM sweep, M={M}: 36 layers x {{qkv 2560->6144, o 4096->2560, "
+                               "gate_up 2560->19456 + SiLU*mul, down 9728->2560}} + lm_head 2560->151936, "
+                               "distinct weights per layer", "M": M, "calls_per_step": 4 * LAYERS + 1,
+                   "bytes_per_step": sweep_bytes, "graph": True},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
+        "lm_head_argmax_matches_torch_gpu": argmax_ok,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_gemm": table,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline(torch, layer0, lm0, x, M, seconds):
+    """The reference's CPU path (torch bf16 F.linear, the oracle's routine) on
+    this host's cores, over one layer's four projections + lm_head at the sweep
+    shape, with the same weight bits as the GPU layer 0."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import gemm_ref as R
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    w = {k: v.cpu() for k, v in layer0.items()}
+    wl = lm0.cpu()
+    xc = {k: v.cpu() for k, v in x.items()}
+    calls = [lambda: R.linear_bf16(xc["qkv"], w["qkv"]), lambda: R.linear_bf16(xc["o"], w["o"]),
+             lambda: R.gateup_bf16(xc["gate_up"], w["gate_up"]), lambda: R.linear_bf16(xc["down"], w["down"]),
+             lambda: R.linear_bf16(xc["lm_head"], wl)]
+    nbytes = sum(algo_bytes(nm, M) for nm in ("qkv", "o", "gate_up", "down", "lm_head"))
+    for c in calls * 2:
+        c()
+    times = []
+    t_end = time.time() + seconds
+    while time.time() < t_end or len(times) < 5:
+        t = time.perf_counter()
+        for c in calls:
+            c()
+        times.append(time.perf_counter() - t)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = platform.processor() or "?"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    gbps = nbytes / med / 1e9
+    log(f"cpu baseline: {med * 1000:.1f} ms per sample, {gbps:.1f} GB/s on {n} threads ({cpu_model})")
+    return {"value": round(gbps, 2), "unit": "GB/s", "cores": n, "kind": "port",
+            "sample": f"torch bf16 F.linear (fp32 accumulate) on host copies of layer 0's qkv, o, gate_up+SiLU*mul, "
+                      f"down and lm_head at M={M} (0.98 GB of weights); median of {len(times)} samples "
+                      f"over ~{seconds:.0f}s after 2 warm-ups; {cpu_model}",
+            "ms_per_sample": round(med * 1000, 2)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

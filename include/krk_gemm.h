@@ -1,0 +1,154 @@
+/*
+ * krk_gemm.h — C ABI of the MI355X (gfx950) skinny decode GEMM.
+ *
+ *   y[M, Nout] = epilogue( x[M, K] · W[N, K]ᵀ )      bf16 in, fp32 accumulate, bf16 out
+ *
+ * All operands are row-major bf16 (raw 16-bit bit patterns) in device memory.
+ * Leading dimensions are in elements.  Nothing in this interface allocates,
+ * synchronises or reads device memory on the host: every call enqueues its
+ * kernels on `stream` and returns, so it may be recorded into a HIP graph.
+ *
+ * Reference interface replaced (willzeng274/kernel-rush-kawk, Python/Triton):
+ *   engine/kernels/gemm.py:332-361  SkinnyMatmul.__init__/__call__  (C = A·Wᵀ)
+ *   engine/kernels/gemm.py:298-329  SkinnyGateUp.__init__/__call__  (swiglu(A·Wgᵀ, A·Wuᵀ))
+ *   engine/kernels/gemm.py:248-281  Gemv.__call__                   (M = 1 row dot products)
+ *   engine/kernels/gemm.py:96-104, 160-170  _sum_kernel / _sum_gateup_kernel (split-K reduce)
+ *   engine/kernels/gateup64.py:59-81        launch_gateup64 (caller-owned output, M = 64)
+ * The reference exposes these as Python callables f(a, w) -> Tensor; the
+ * Python mirror in kernel-rush-kawk_amd/kernels/gemm.py keeps that surface on
+ * top of this ABI.
+ */
+#ifndef KRK_GEMM_H
+#define KRK_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Epilogues applied to the fp32 accumulators before the bf16 store. */
+enum {
+    /* y = bf16(x·Wᵀ).  Nout = N. */
+    KRK_EPILOGUE_NONE = 0,
+    /* Fused gate/up + SwiGLU.  W rows [0, N/2) are the gate projection and rows
+     * [N/2, N) the up projection (concatenation order of engine/model.py:116);
+     * y[M, N/2] = bf16(bf16(silu_f32(bf16(g))) · bf16(u)), the three roundings
+     * of engine/kernels/gemm.py:107-113 and engine/kernels/swiglu.py:14-24.
+     * N must be even. */
+    KRK_EPILOGUE_SILU_MUL = 1
+};
+
+/* Return codes (0 = success, negative = error; krk_last_error() explains). */
+enum {
+    KRK_OK = 0,
+    KRK_ERR_INVALID = -1,     /* bad shape, stride, epilogue or null pointer */
+    KRK_ERR_ALIGN = -2,       /* base pointer or leading dimension not 16-byte aligned */
+    KRK_ERR_ALIAS = -3,       /* y overlaps x, W or the workspace */
+    KRK_ERR_WORKSPACE = -4,   /* workspace missing or smaller than krk_gemm_workspace_bytes() */
+    KRK_ERR_HIP = -5,         /* the HIP runtime rejected a launch */
+    KRK_ERR_UNSUPPORTED = -6  /* a forced configuration this build does not provide */
+};
+
+/*
+ * krk_gemm_bf16 — one projection call.
+ *
+ * Replaces SkinnyMatmul.__call__ (engine/kernels/gemm.py:346-361) and
+ * SkinnyGateUp.__call__ (engine/kernels/gemm.py:314-329): the reference
+ * allocates `c` and launches _skinny_kernel / _gateup_kernel plus the split-K
+ * sum; here the caller owns y and the split-K workspace.
+ *
+ *   x          [M, K] bf16, row stride ldx >= K, ldx % 8 == 0, 16-byte aligned
+ *   w          [N, K] bf16, row stride ldw >= K, ldw % 8 == 0, 16-byte aligned
+ *   y          [M, Nout] bf16, row stride ldy >= Nout; must not overlap x, w or workspace
+ *   M >= 1 (rows beyond 64 are processed in chunks of 64), N >= 1, K >= 8, K % 8 == 0
+ *   epilogue   KRK_EPILOGUE_NONE or KRK_EPILOGUE_SILU_MUL
+ *   workspace  device memory of at least krk_gemm_workspace_bytes(M, N, K, epilogue)
+ *              bytes (may be NULL when that is 0).  It must be zero-filled once
+ *              before its first use; every call leaves it zero-filled again.
+ *              Calls that share one workspace must be ordered on one stream.
+ *   stream     hipStream_t (NULL = the default stream)
+ *
+ * Results are deterministic: the same inputs and shape give bit-identical y.
+ */
+int krk_gemm_bf16(const void* x, int64_t ldx,
+                  const void* w, int64_t ldw,
+                  void* y, int64_t ldy,
+                  int M, int N, int K, int epilogue,
+                  void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/*
+ * krk_gemm_workspace_bytes — split-K scratch needed by krk_gemm_bf16 for this
+ * shape (0 when the chosen plan does not split K).  Replaces the per-object
+ * partial-sum allocation of SkinnyMatmul.__init__ (engine/kernels/gemm.py:341)
+ * and SkinnyGateUp.__init__ (engine/kernels/gemm.py:309).  Returns 0 for an
+ * invalid shape as well; krk_gemm_bf16 then reports the shape error.
+ */
+size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue);
+
+/*
+ * Kernel configuration.  Mirrors the per-candidate config dicts of the
+ * reference (engine/kernels/gemm.py:284-288 GEMV_CONFIGS, :364-375 CONFIGS)
+ * that SkinnyMatmul/Gemv are constructed from (gemm.py:251, 301, 333).
+ * A field left at 0 takes the dispatcher's choice for this shape.
+ */
+enum {
+    KRK_KERNEL_AUTO = 0,
+    KRK_KERNEL_MFMA = 1,   /* bf16 MFMA 16x16x32 tiles, W fragments straight from HBM */
+    KRK_KERNEL_VALU = 2    /* VALU dot2 row streaming, x staged in LDS (M <= 8) */
+};
+
+typedef struct krk_gemm_config {
+    int kernel;   /* KRK_KERNEL_* */
+    int m_tiles;  /* MFMA: 16-row x tiles per wave, covering M (1..4); VALU: ignored */
+    int n_tiles;  /* MFMA: 16-row W tiles per wave (1, 2, 4; even with SILU_MUL);
+                     VALU: W rows per wave (1, 2, 4) */
+    int unroll;   /* k-steps loaded per pipeline stage (MFMA: 2, 4, 8; VALU: 1, 2, 4) */
+    int waves;    /* waves per workgroup (1, 2, 4, 8) */
+    int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
+} krk_gemm_config;
+
+/*
+ * krk_gemm_plan — the configuration krk_gemm_bf16 uses for this shape (the
+ * static shape -> kernel table that stands in for the reference's warm-up
+ * pickers, engine/kernels/gemm.py:417-458, 461-498).  Returns KRK_OK or a
+ * negative error for an invalid shape.
+ */
+int krk_gemm_plan(int M, int N, int K, int epilogue, krk_gemm_config* out);
+
+/*
+ * krk_gemm_config_workspace_bytes — as krk_gemm_workspace_bytes, for an
+ * explicit configuration (0 fields filled from krk_gemm_plan).
+ */
+size_t krk_gemm_config_workspace_bytes(int M, int N, int K, int epilogue,
+                                       const krk_gemm_config* cfg);
+
+/*
+ * krk_gemm_bf16_config — krk_gemm_bf16 with an explicit configuration, the
+ * counterpart of calling one candidate SkinnyMatmul(M, N, K, device, **cfg)
+ * (engine/kernels/gemm.py:427-448).  Every configuration computes the same
+ * function; they differ only in fp32 summation order.  Returns
+ * KRK_ERR_UNSUPPORTED for a combination this build does not instantiate.
+ */
+int krk_gemm_bf16_config(const void* x, int64_t ldx,
+                         const void* w, int64_t ldw,
+                         void* y, int64_t ldy,
+                         int M, int N, int K, int epilogue,
+                         const krk_gemm_config* cfg,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
+ * krk_last_error — text of the last error raised on the calling thread by
+ * any krk_* function ("" if none).  Stands in for the ValueError messages of
+ * engine/kernels/gateup64.py:63-74 and engine/kernels/gemm.py:253-254.
+ */
+const char* krk_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KRK_GEMM_H */

@@ -1,0 +1,325 @@
+// C ABI of the gfx950 skinny decode GEMM (declared in include/krk_gemm.h).
+//
+// Host responsibilities: argument validation (the reference's launchers raise
+// ValueError for these, engine/kernels/gateup64.py:63-74,
+// engine/kernels/gemm.py:253-254), the static shape -> configuration table
+// that replaces the warm-up pickers (engine/kernels/gemm.py:417-498), and
+// stream-ordered kernel launches.  Nothing here allocates, synchronises or
+// touches device memory from the host, so every call is graph-capturable.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "krk_gemm.h"
+#include "krk_mfma.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+constexpr int kMaxRowsPerLaunch = 64;
+constexpr int kValuMaxRows = 8;
+constexpr int kCuCount = 256;  // MI355X: 8 XCDs x 32 CUs
+// LDS per workgroup this build plans for (the portable 64 KB), and what the
+// kernels' static __shared__ variables take beside the dynamic reduction area.
+constexpr size_t kLdsBudget = 65536;
+constexpr size_t kLdsReserve = 256;
+
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+bool valid_epilogue(int e) { return e == KRK_EPILOGUE_NONE || e == KRK_EPILOGUE_SILU_MUL; }
+
+int check_shape(int M, int N, int K, int epilogue) {
+    if (M < 1 || N < 1 || K < 8) return fail(KRK_ERR_INVALID, "shape M=%d N=%d K=%d: need M >= 1, N >= 1, K >= 8", M, N, K);
+    if (K % 8) return fail(KRK_ERR_INVALID, "K=%d must be a multiple of 8 (16-byte rows)", K);
+    if (!valid_epilogue(epilogue)) return fail(KRK_ERR_INVALID, "unknown epilogue %d", epilogue);
+    if (epilogue == KRK_EPILOGUE_SILU_MUL && (N % 2)) return fail(KRK_ERR_INVALID, "SILU_MUL needs an even N (gate rows then up rows), got N=%d", N);
+    return KRK_OK;
+}
+
+// Channels of output per block and block count for a configuration.
+struct Geometry {
+    int Mc;       // rows per launch
+    int Nout;     // output columns
+    int cb;       // output channels per block
+    int nblocks;  // blocks along N
+};
+
+Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
+    Geometry g;
+    g.Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
+    g.Nout = silu ? N / 2 : N;
+    if (c.kernel == KRK_KERNEL_VALU) {
+        g.cb = c.waves * c.n_tiles;  // one group of n_tiles channels per wave
+    } else {
+        g.cb = 16 * (silu ? c.n_tiles / 2 : c.n_tiles);
+    }
+    g.nblocks = cdiv(g.Nout, g.cb);
+    return g;
+}
+
+// The dispatch table.  Every projection is HBM-bound (arithmetic intensity is
+// about M flop/byte); the table only decides how the weight stream is cut so
+// all 256 CUs stream from the first cycle.
+void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
+    const int Nout = silu ? N / 2 : N;
+    const int KS = cdiv(K, 32);
+    krk_gemm_config r{};
+    r.kernel = KRK_KERNEL_MFMA;
+    r.m_tiles = cdiv(Mc, 16);
+    r.n_tiles = silu ? 2 : (Mc <= 16 ? 1 : 2);
+    r.unroll = r.m_tiles == 1 ? 8 : 4;
+    r.waves = 4;
+    const int cb = 16 * (silu ? r.n_tiles / 2 : r.n_tiles);
+    const int nblocks = cdiv(Nout, cb);
+    int splits = 1;
+    while (nblocks * splits < 2 * kCuCount && splits < 8 &&
+           KS / (2 * splits * r.waves) >= r.unroll)
+        splits *= 2;
+    r.splits = splits;
+    *c = r;
+}
+
+// Fill the zero fields of a caller's configuration from the table and check
+// that the result is one this build instantiates.
+int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in, krk_gemm_config* out) {
+    krk_gemm_config a;
+    auto_config(M, N, K, epilogue, &a);
+    if (!in) { *out = a; return KRK_OK; }
+    krk_gemm_config c = *in;
+    if (c.kernel == KRK_KERNEL_AUTO) c.kernel = a.kernel;
+    const bool same_kernel = c.kernel == a.kernel;
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    if (c.kernel == KRK_KERNEL_MFMA) {
+        if (!c.m_tiles) c.m_tiles = cdiv(Mc, 16);
+        if (!c.n_tiles) c.n_tiles = same_kernel ? a.n_tiles : (epilogue == KRK_EPILOGUE_SILU_MUL ? 2 : 1);
+        if (!c.unroll) c.unroll = same_kernel ? a.unroll : 4;
+        if (!c.waves) c.waves = same_kernel ? a.waves : 4;
+        if (!c.splits) c.splits = same_kernel ? a.splits : 1;
+        if (c.m_tiles < cdiv(Mc, 16) || c.m_tiles > 4)
+            return fail(KRK_ERR_INVALID, "m_tiles=%d cannot cover %d rows (need %d..4)", c.m_tiles, Mc, cdiv(Mc, 16));
+        if (c.n_tiles != 1 && c.n_tiles != 2 && c.n_tiles != 4)
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA n_tiles=%d not in {1,2,4}", c.n_tiles);
+        if (epilogue == KRK_EPILOGUE_SILU_MUL && c.n_tiles % 2)
+            return fail(KRK_ERR_UNSUPPORTED, "SILU_MUL needs an even n_tiles, got %d", c.n_tiles);
+        if (c.unroll != 2 && c.unroll != 4 && c.unroll != 8)
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA unroll=%d not in {2,4,8}", c.unroll);
+        if (c.waves > 0 && (size_t)c.waves * c.m_tiles * c.n_tiles * 1024 + kLdsReserve > kLdsBudget)
+            return fail(KRK_ERR_UNSUPPORTED, "waves*m_tiles*n_tiles=%d KB of reduction LDS exceeds the %zu-byte budget",
+                        c.waves * c.m_tiles * c.n_tiles, kLdsBudget);
+    } else if (c.kernel == KRK_KERNEL_VALU) {
+        if (Mc > kValuMaxRows)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU kernel handles M <= %d, got %d", kValuMaxRows, M);
+        c.m_tiles = 0;
+        if (!c.n_tiles) c.n_tiles = 1;
+        if (!c.unroll) c.unroll = 1;
+        if (!c.waves) c.waves = 4;
+        if (!c.splits) c.splits = 1;
+        if (c.n_tiles != 1 && c.n_tiles != 2 && c.n_tiles != 4)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles=%d not in {1,2,4}", c.n_tiles);
+        if (c.unroll != 1 && c.unroll != 2 && c.unroll != 4)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU unroll=%d not in {1,2,4}", c.unroll);
+    } else {
+        return fail(KRK_ERR_UNSUPPORTED, "unknown kernel %d", c.kernel);
+    }
+    if (c.waves != 1 && c.waves != 2 && c.waves != 4)
+        return fail(KRK_ERR_UNSUPPORTED, "waves=%d not in {1,2,4}", c.waves);
+    if (c.splits < 1 || c.splits > 32)
+        return fail(KRK_ERR_UNSUPPORTED, "splits=%d not in 1..32", c.splits);
+    *out = c;
+    return KRK_OK;
+}
+
+// Workspace layout: [block counters, padded to 256 B][fp32 partials splits x Mc x N].
+size_t workspace_for(int M, int N, int epilogue, const krk_gemm_config& c) {
+    if (c.splits <= 1) return 0;
+    const Geometry g = geometry(M, N, epilogue, c);
+    return align_up((size_t)g.nblocks * sizeof(uint32_t), 256) +
+           (size_t)c.splits * (size_t)g.Mc * (size_t)N * sizeof(float);
+}
+
+bool overlaps(uintptr_t a0, uintptr_t a1, uintptr_t b0, uintptr_t b1) { return a0 < b1 && b0 < a1; }
+
+struct LaunchArgs {
+    const uint16_t* x;
+    int64_t ldx;
+    const uint16_t* w;
+    int64_t ldw;
+    uint16_t* y;
+    int64_t ldy;
+    int M, N, K, splits;
+    float* part;
+    uint32_t* ctr;
+};
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return KRK_OK;
+    return fail(KRK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+template <int MT, int NT, int U, bool SILU>
+int launch_mfma(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream) {
+    void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
+                    (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr};
+    const size_t shm = (size_t)waves * MT * NT * 64 * sizeof(krk::f32x4);
+    hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&krk::mfma_gemm_kernel<MT, NT, U, SILU>),
+                                   dim3(nblocks * a.splits), dim3(64 * waves), args, shm, stream);
+    return hip_status(e, "mfma_gemm_kernel launch");
+}
+
+template <int MT, int NT, bool SILU>
+int dispatch_mfma_u(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    switch (c.unroll) {
+        case 2: return launch_mfma<MT, NT, 2, SILU>(a, nblocks, c.waves, s);
+        case 4: return launch_mfma<MT, NT, 4, SILU>(a, nblocks, c.waves, s);
+        case 8: return launch_mfma<MT, NT, 8, SILU>(a, nblocks, c.waves, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA unroll=%d", c.unroll);
+}
+
+template <int MT, bool SILU>
+int dispatch_mfma_n(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    if constexpr (!SILU) {
+        if (c.n_tiles == 1) return dispatch_mfma_u<MT, 1, false>(a, c, nblocks, s);
+    }
+    if (c.n_tiles == 2) return dispatch_mfma_u<MT, 2, SILU>(a, c, nblocks, s);
+    if (c.n_tiles == 4) return dispatch_mfma_u<MT, 4, SILU>(a, c, nblocks, s);
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA n_tiles=%d", c.n_tiles);
+}
+
+template <bool SILU>
+int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    switch (c.m_tiles) {
+        case 1: return dispatch_mfma_n<1, SILU>(a, c, nblocks, s);
+        case 2: return dispatch_mfma_n<2, SILU>(a, c, nblocks, s);
+        case 3: return dispatch_mfma_n<3, SILU>(a, c, nblocks, s);
+        case 4: return dispatch_mfma_n<4, SILU>(a, c, nblocks, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
+}
+
+template <bool SILU>
+int dispatch_valu(const LaunchArgs&, const krk_gemm_config&, int, hipStream_t) {
+    return fail(KRK_ERR_UNSUPPORTED, "VALU kernel not built yet");
+}
+
+int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+              int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
+              void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    if (!x || !w || !y) return fail(KRK_ERR_INVALID, "null operand pointer (x=%p w=%p y=%p)", x, w, y);
+    const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
+    const int Nout = silu ? N / 2 : N;
+    if (ldx < K || ldw < K) return fail(KRK_ERR_INVALID, "ldx=%lld / ldw=%lld must be >= K=%d", (long long)ldx, (long long)ldw, K);
+    if (ldy < Nout) return fail(KRK_ERR_INVALID, "ldy=%lld must be >= %d output columns", (long long)ldy, Nout);
+    if ((ldx % 8) || (ldw % 8)) return fail(KRK_ERR_ALIGN, "ldx=%lld and ldw=%lld must be multiples of 8 elements", (long long)ldx, (long long)ldw);
+    if (((uintptr_t)x % 16) || ((uintptr_t)w % 16)) return fail(KRK_ERR_ALIGN, "x=%p and w=%p must be 16-byte aligned", x, w);
+    if ((uintptr_t)y % 2) return fail(KRK_ERR_ALIGN, "y=%p must be 2-byte aligned", y);
+
+    krk_gemm_config c;
+    rc = resolve_config(M, N, K, epilogue, cfg, &c);
+    if (rc) return rc;
+
+    const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((uint64_t)(M - 1) * ldx + K) * 2;
+    const uintptr_t w0 = (uintptr_t)w, w1 = w0 + ((uint64_t)(N - 1) * ldw + K) * 2;
+    const uintptr_t y0 = (uintptr_t)y, y1 = y0 + ((uint64_t)(M - 1) * ldy + Nout) * 2;
+    if (overlaps(y0, y1, x0, x1) || overlaps(y0, y1, w0, w1))
+        return fail(KRK_ERR_ALIAS, "output y may not share memory with x or W");
+
+    const size_t need = workspace_for(M, N, epilogue, c);
+    if (need) {
+        if (!workspace) return fail(KRK_ERR_WORKSPACE, "this plan needs a %zu-byte workspace, got none", need);
+        if (workspace_bytes < need) return fail(KRK_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, need);
+        if ((uintptr_t)workspace % 16) return fail(KRK_ERR_ALIGN, "workspace=%p must be 16-byte aligned", workspace);
+        const uintptr_t s0 = (uintptr_t)workspace, s1 = s0 + need;
+        if (overlaps(s0, s1, x0, x1) || overlaps(s0, s1, w0, w1) || overlaps(s0, s1, y0, y1))
+            return fail(KRK_ERR_ALIAS, "workspace may not share memory with x, W or y");
+    }
+
+    const Geometry g = geometry(M, N, epilogue, c);
+    uint32_t* ctr = need ? static_cast<uint32_t*>(workspace) : nullptr;
+    float* part = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                  align_up((size_t)g.nblocks * sizeof(uint32_t), 256))
+                       : nullptr;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int m0 = 0; m0 < M; m0 += kMaxRowsPerLaunch) {
+        LaunchArgs a;
+        a.x = static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx;
+        a.ldx = ldx;
+        a.w = static_cast<const uint16_t*>(w);
+        a.ldw = ldw;
+        a.y = static_cast<uint16_t*>(y) + (int64_t)m0 * ldy;
+        a.ldy = ldy;
+        a.M = (M - m0) < kMaxRowsPerLaunch ? (M - m0) : kMaxRowsPerLaunch;
+        a.N = N;
+        a.K = K;
+        a.splits = c.splits;
+        a.part = part;
+        a.ctr = ctr;
+        if (c.kernel == KRK_KERNEL_MFMA) {
+            rc = silu ? dispatch_mfma<true>(a, c, g.nblocks, st) : dispatch_mfma<false>(a, c, g.nblocks, st);
+        } else {
+            rc = silu ? dispatch_valu<true>(a, c, g.nblocks, st) : dispatch_valu<false>(a, c, g.nblocks, st);
+        }
+        if (rc) return rc;
+    }
+    return KRK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int krk_gemm_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                  int M, int N, int K, int epilogue, void* workspace, size_t workspace_bytes, void* stream) {
+    return gemm_impl(x, ldx, w, ldw, y, ldy, M, N, K, epilogue, nullptr, workspace, workspace_bytes, stream);
+}
+
+int krk_gemm_bf16_config(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                         int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    return gemm_impl(x, ldx, w, ldw, y, ldy, M, N, K, epilogue, cfg, workspace, workspace_bytes, stream);
+}
+
+size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue) {
+    if (check_shape(M, N, K, epilogue)) return 0;
+    krk_gemm_config c;
+    auto_config(M, N, K, epilogue, &c);
+    return workspace_for(M, N, epilogue, c);
+}
+
+size_t krk_gemm_config_workspace_bytes(int M, int N, int K, int epilogue, const krk_gemm_config* cfg) {
+    if (check_shape(M, N, K, epilogue)) return 0;
+    krk_gemm_config c;
+    if (resolve_config(M, N, K, epilogue, cfg, &c)) return 0;
+    return workspace_for(M, N, epilogue, c);
+}
+
+int krk_gemm_plan(int M, int N, int K, int epilogue, krk_gemm_config* out) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    if (!out) return fail(KRK_ERR_INVALID, "null output config");
+    auto_config(M, N, K, epilogue, out);
+    return KRK_OK;
+}
+
+const char* krk_last_error(void) { return g_err; }
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+"""ctypes binding of libkrk_gemm.so (C ABI declared in include/krk_gemm.h).
+
+torch is imported first so that its HIP runtime (soname libamdhip64.so.7) is
+the one the library binds to; the process then has a single HIP runtime.
+Loading fails loudly when the library has not been built: there is no
+fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "libkrk_gemm.so"
+
+KRK_OK = 0
+KRK_ERR_INVALID = -1
+KRK_ERR_ALIGN = -2
+KRK_ERR_ALIAS = -3
+KRK_ERR_WORKSPACE = -4
+KRK_ERR_HIP = -5
+KRK_ERR_UNSUPPORTED = -6
+
+EPILOGUE_NONE = 0
+EPILOGUE_SILU_MUL = 1
+
+KERNEL_AUTO = 0
+KERNEL_MFMA = 1
+KERNEL_VALU = 2
+
+#: Every function the header declares, with (restype, argtypes).
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_size = ctypes.c_size_t
+
+
+class GemmConfig(ctypes.Structure):
+    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits."""
+
+    _fields_ = [
+        ("kernel", _int),
+        ("m_tiles", _int),
+        ("n_tiles", _int),
+        ("unroll", _int),
+        ("waves", _int),
+        ("splits", _int),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+    @classmethod
+    def from_dict(cls, d: dict | None) -> "GemmConfig":
+        c = cls()
+        for k, v in (d or {}).items():
+            if k not in dict(cls._fields_):
+                raise ValueError(f"unknown config field {k!r}")
+            setattr(c, k, int(v))
+        return c
+
+
+SIGNATURES = {
+    "krk_gemm_bf16": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
+                              _int, _int, _int, _int, _c_void_p, _size, _c_void_p]),
+    "krk_gemm_workspace_bytes": (_size, [_int, _int, _int, _int]),
+    "krk_gemm_plan": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_config_workspace_bytes": (_size, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_bf16_config": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
+                                     _int, _int, _int, _int, ctypes.POINTER(GemmConfig),
+                                     _c_void_p, _size, _c_void_p]),
+    "krk_last_error": (ctypes.c_char_p, []),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library.  Raises ImportError if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ImportError(
+                    f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                    "or `python kernel-rush-kawk_amd/build_lib.py` (there is no fallback GEMM)")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().krk_last_error().decode(errors="replace")
+
+
+class KrkError(RuntimeError):
+    """A krk_* call returned an error code; ``code`` is the KRK_ERR_* value."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"krk error {code}: {msg}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    """Raise for a non-zero krk return code.  Argument errors (invalid shape,
+    alignment, aliasing, workspace) raise ValueError like the reference's
+    launchers (engine/kernels/gateup64.py:63-74); runtime errors RuntimeError."""
+    if rc == KRK_OK:
+        return
+    msg = last_error()
+    if rc in (KRK_ERR_INVALID, KRK_ERR_ALIGN, KRK_ERR_ALIAS, KRK_ERR_WORKSPACE, KRK_ERR_UNSUPPORTED):
+        raise ValueError(f"krk error {rc}: {msg}")
+    raise KrkError(rc, msg)

@@ -1,0 +1,283 @@
+"""Skinny decode GEMM for Qwen3-4B on MI355X: ``C[M, N] = A[M, K] @ W[N, K]^T``.
+
+Python surface of libkrk_gemm.so, shaped like the reference's
+``engine/kernels/gemm.py`` so an engine can swap it in unchanged:
+
+* :class:`SkinnyMatmul` — ``f(a, w) -> a @ w.T`` as a new bf16 tensor
+  (reference ``SkinnyMatmul``, engine/kernels/gemm.py:332-361);
+* :class:`SkinnyGateUp` — ``f(a, wgu) -> silu(a @ Wg.T) * (a @ Wu.T)`` over the
+  concatenated gate-then-up weight (reference ``SkinnyGateUp``,
+  engine/kernels/gemm.py:298-329, plus ``swiglu``, engine/kernels/swiglu.py);
+* :func:`pick_matmul` / :func:`pick_gateup` — per-shape callables validated
+  at warm-up against ``torch.nn.functional.linear`` on the same device
+  (reference pickers, engine/kernels/gemm.py:417-498);
+* :func:`_time` — CUDA/HIP-graph replay timer (engine/kernels/gemm.py:378-414).
+
+All compute runs in the HIP kernels of libkrk_gemm.so; nothing here falls
+back to another GEMM.  Calls launch on torch's current stream, allocate only
+their output tensor, never synchronise, and may be captured in a graph.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
+
+__all__ = [
+    "SkinnyMatmul", "SkinnyGateUp", "Gemv", "pick_matmul", "pick_gateup", "plan", "gemm_into", "_time",
+]
+
+
+def plan(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE) -> dict:
+    """The configuration the library's dispatch table uses for this shape."""
+    cfg = GemmConfig()
+    _lib.check(_lib.load().krk_gemm_plan(M, N, K, epilogue, ctypes.byref(cfg)))
+    return cfg.as_dict()
+
+
+def _check_operand(name: str, t: torch.Tensor, rows: int | None, cols: int) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if rows is not None and t.shape[0] != rows:
+        raise ValueError(f"{name} must have {rows} rows, got shape {tuple(t.shape)}")
+    if t.shape[1] != cols:
+        raise ValueError(f"{name} must have {cols} columns, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1:
+        raise ValueError(f"{name} rows must be contiguous (stride(1) == 1), got strides {t.stride()}")
+
+
+def gemm_into(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, epilogue: int = EPILOGUE_NONE,
+              workspace: torch.Tensor | None = None, config: dict | None = None) -> torch.Tensor:
+    """Allocation-free call: ``y = epilogue(x @ w.T)`` into the caller's ``y``.
+
+    Counterpart of the reference's caller-owned-output launcher
+    (``launch_gateup64``, engine/kernels/gateup64.py:59-81).  ``workspace`` must
+    hold at least ``workspace_bytes`` bytes of zero-filled device memory when
+    the plan splits K.
+    """
+    M, K = x.shape
+    N = w.shape[0]
+    _check_operand("x", x, None, K)
+    _check_operand("w", w, None, K)
+    nout = N // 2 if epilogue == EPILOGUE_SILU_MUL else N
+    _check_operand("y", y, M, nout)
+    for name, t in (("x", x), ("w", w), ("y", y)):
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must be a GPU tensor, got device {t.device}")
+    if not (x.device == w.device == y.device):
+        raise ValueError(f"operands on different devices: {x.device}, {w.device}, {y.device}")
+    ws_ptr, ws_bytes = 0, 0
+    if workspace is not None:
+        if workspace.device != x.device:
+            raise ValueError("workspace must be on the operands' device")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        if config is None:
+            rc = lib.krk_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0),
+                                   M, N, K, epilogue, ws_ptr, ws_bytes, stream)
+        else:
+            cfg = GemmConfig.from_dict(config)
+            rc = lib.krk_gemm_bf16_config(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
+                                          y.stride(0), M, N, K, epilogue, ctypes.byref(cfg), ws_ptr, ws_bytes, stream)
+    _lib.check(rc)
+    return y
+
+
+def workspace_bytes(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE, config: dict | None = None) -> int:
+    lib = _lib.load()
+    if config is None:
+        return int(lib.krk_gemm_workspace_bytes(M, N, K, epilogue))
+    cfg = GemmConfig.from_dict(config)
+    return int(lib.krk_gemm_config_workspace_bytes(M, N, K, epilogue, ctypes.byref(cfg)))
+
+
+class SkinnyMatmul:
+    """``c = a @ w.T`` for a fixed (M, N, K): bf16 in, fp32 accumulation, bf16 out.
+
+    Mirrors the reference's ``SkinnyMatmul`` (engine/kernels/gemm.py:332-361):
+    the split-K workspace belongs to the object and is allocated (zero-filled)
+    once here; each call allocates only its output.  ``config`` optionally
+    forces a kernel configuration (keys of ``krk_gemm_config``).
+    """
+
+    epilogue = EPILOGUE_NONE
+
+    def __init__(self, M: int, N: int, K: int, device, config: dict | None = None):
+        if M < 1 or N < 1 or K < 8 or K % 8:
+            raise ValueError(f"unsupported shape M={M} N={N} K={K} (need K >= 8, K % 8 == 0)")
+        self.M, self.N, self.K = M, N, K
+        self.device = torch.device(device)
+        self.config = dict(config) if config else None
+        # An invalid explicit config also reports 0 here; the first call then
+        # raises ValueError with the library's explanation.
+        nbytes = workspace_bytes(M, N, K, self.epilogue, self.config)
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device) if nbytes else None
+        self.out_cols = N // 2 if self.epilogue == EPILOGUE_SILU_MUL else N
+
+    @property
+    def resolved_config(self) -> dict:
+        if self.config is None:
+            return plan(self.M, self.N, self.K, self.epilogue)
+        return dict(self.config)
+
+    def run(self, a: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """Allocation-free form: write into ``out``."""
+        if a.shape[0] != self.M or a.shape[1] != self.K or w.shape[0] != self.N:
+            raise ValueError(f"operands {tuple(a.shape)} x {tuple(w.shape)} do not match the "
+                             f"({self.M}, {self.N}, {self.K}) this object was built for")
+        return gemm_into(a, w, out, self.epilogue, self.workspace, self.config)
+
+    def __call__(self, a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        out = torch.empty((self.M, self.out_cols), dtype=torch.bfloat16, device=a.device)
+        return self.run(a, w, out)
+
+
+class SkinnyGateUp(SkinnyMatmul):
+    """``silu(a @ Wg.T) * (a @ Wu.T)`` in one pass over the concatenated weight.
+
+    ``I`` is the intermediate width; the weight is ``[2*I, K]`` with the gate
+    rows first (engine/model.py:116).  Rounding follows the reference's three
+    bf16 boundaries (engine/kernels/gemm.py:107-113).  Call as ``f(a, wgu)`` or,
+    like the reference (engine/kernels/gemm.py:314), ``f(a, wg, wu)`` with
+    ``wg = wgu[:I]`` and ``wu = wgu[I:]`` views of one tensor.
+    """
+
+    epilogue = EPILOGUE_SILU_MUL
+
+    def __init__(self, M: int, I: int, K: int, device, config: dict | None = None):
+        self.I = I
+        super().__init__(M, 2 * I, K, device, config)
+
+    def __call__(self, a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor | None = None) -> torch.Tensor:
+        wgu = wg if wu is None else _join_halves(wg, wu, self.I)
+        return super().__call__(a, wgu)
+
+
+def _join_halves(wg: torch.Tensor, wu: torch.Tensor, I: int) -> torch.Tensor:
+    """The concatenated ``[2I, K]`` view behind ``wg = wgu[:I]``, ``wu = wgu[I:]``."""
+    if wg.shape != wu.shape or wg.shape[0] != I or wg.stride() != wu.stride():
+        raise ValueError("wg and wu must be the two halves of one [2*I, K] weight")
+    gap = (wu.data_ptr() - wg.data_ptr()) // wg.element_size()
+    if gap != I * wg.stride(0):
+        raise ValueError("wu must start right after wg's I rows (wg = wgu[:I], wu = wgu[I:])")
+    return torch.as_strided(wg, (2 * I, wg.shape[1]), wg.stride())
+
+
+class Gemv(SkinnyMatmul):
+    """M = 1 row dot products (reference ``Gemv``, engine/kernels/gemm.py:248-281).
+    ``gateup=True`` applies the SwiGLU epilogue like the reference's GATEUP mode."""
+
+    def __init__(self, M: int, N: int, K: int, device, gateup: bool = False, config: dict | None = None):
+        if M > 4:
+            raise ValueError("Gemv handles at most 4 rows")
+        self.epilogue = EPILOGUE_SILU_MUL if gateup else EPILOGUE_NONE
+        super().__init__(M, 2 * N if gateup else N, K, device, config)
+        self.I = N
+
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, w2: torch.Tensor | None = None) -> torch.Tensor:
+        if self.epilogue == EPILOGUE_SILU_MUL:
+            w = w if w2 is None else _join_halves(w, w2, self.I)
+        return super().__call__(a, w)
+
+
+def _time(fn, iters: int = 30, rotate: list | None = None) -> float:
+    """Average milliseconds per call, measured as a graph replay.
+
+    Same method as the reference (engine/kernels/gemm.py:378-414): 3 warm-up
+    calls on a side stream, ``iters`` calls captured in one graph (rotating
+    over ``rotate`` so consecutive calls stream distinct weights), the median
+    of 5 timed replays divided by ``iters``.
+    """
+    ws = rotate or [None]
+    call = (lambda i: fn(ws[i % len(ws)])) if rotate else (lambda i: fn())
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(3):
+            call(i)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(iters):
+            call(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(5):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        samples.append(start.elapsed_time(end) / iters)
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def _validate(out: torch.Tensor, ref: torch.Tensor, what: str, log=None) -> None:
+    """Reference acceptance rule (engine/kernels/gemm.py:441-447): max error
+    within ``0.02 * max|ref| + 1e-3``.  A failure raises instead of falling back."""
+    out, ref = out.float(), ref.float()
+    err = (out - ref).abs().max().item()
+    tol = 0.02 * ref.abs().max().item() + 1e-3
+    if not (err <= tol):
+        raise RuntimeError(f"{what}: HIP GEMM disagrees with F.linear (err {err:.4g} > tol {tol:.4g})")
+    if log:
+        log(f"{what}: validated (err {err:.3g} <= {tol:.3g})")
+
+
+def _linear_fp32acc(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """torch GEMM with fp32 accumulation forced (the validation reference)."""
+    prev = torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction
+    torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+    try:
+        return F.linear(a, w)
+    finally:
+        torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = prev
+
+
+def _silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    I = gu.shape[1] // 2
+    return F.silu(gu[:, :I]) * gu[:, I:]
+
+
+def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = None):
+    """Return ``f(a, w) -> a @ w.T`` for this exact shape (reference
+    engine/kernels/gemm.py:417-458).  The HIP kernel is validated once against
+    ``F.linear`` on the same inputs; with ``log`` its graph-replay time over
+    the ``ws`` rotation is reported in µs and GB/s."""
+    M, K = a.shape
+    N = w.shape[0]
+    mm = SkinnyMatmul(M, N, K, a.device)
+    _validate(mm(a, w), _linear_fp32acc(a, w), f"matmul M={M} N={N} K={K}", log)
+    if log:
+        ms = _time(lambda w_: mm(a, w_), rotate=ws or [w])
+        log(f"matmul M={M} N={N} K={K}: krk{mm.resolved_config} {ms * 1000:.1f}us "
+            f"({2 * M * N * K / ms / 1e6:.0f} GFLOP/s, {N * K * 2 / ms / 1e6:.0f} GB/s)")
+    return mm
+
+
+def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = None):
+    """Return ``f(a, wgu) -> silu(a @ Wg.T) * (a @ Wu.T)`` (reference
+    engine/kernels/gemm.py:461-498), validated against ``swiglu(F.linear)``."""
+    M, K = a.shape
+    I = wgu.shape[0] // 2
+    mm = SkinnyGateUp(M, I, K, a.device)
+    _validate(mm(a, wgu), _silu_mul(_linear_fp32acc(a, wgu)), f"gateup M={M} I={I} K={K}", log)
+    if log:
+        ms = _time(lambda w_: mm(a, w_), rotate=ws or [wgu])
+        log(f"gateup M={M} I={I} K={K}: krk{mm.resolved_config} {ms * 1000:.1f}us "
+            f"({2 * I * K * 2 / ms / 1e6:.0f} GB/s)")
+    return mm

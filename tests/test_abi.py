@@ -1,0 +1,185 @@
+"""The C-ABI library without a GPU: it loads, exports every symbol the header
+declares, and rejects bad arguments with the documented error codes before
+touching the device (no call here reaches a kernel launch)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kernels import _lib
+from kernels._lib import GemmConfig
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "krk_gemm.h"
+
+NONE, SILU = _lib.EPILOGUE_NONE, _lib.EPILOGUE_SILU_MUL
+# Fake, well-aligned device addresses far apart: validation never dereferences them.
+X, W, Y, WS = 0x10000000, 0x20000000, 0x30000000, 0x40000000
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(krk_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_surface():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} is declared in krk_gemm.h but not exported"
+
+
+def call(lib, x=X, ldx=2560, w=W, ldw=2560, y=Y, ldy=None, M=1, N=6144, K=2560, epi=NONE, ws=0, wsb=0):
+    if ldy is None:
+        ldy = N // 2 if epi == SILU else N
+    return lib.krk_gemm_bf16(x, ldx, w, ldw, y, ldy, M, N, K, epi, ws, wsb, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(M=0), _lib.KRK_ERR_INVALID, "M >= 1"),
+    (dict(N=0), _lib.KRK_ERR_INVALID, "N >= 1"),
+    (dict(K=4, ldx=8, ldw=8), _lib.KRK_ERR_INVALID, "K >= 8"),
+    (dict(K=2564, ldx=2568, ldw=2568), _lib.KRK_ERR_INVALID, "multiple of 8"),
+    (dict(epi=7), _lib.KRK_ERR_INVALID, "epilogue"),
+    (dict(epi=SILU, N=19455, ldy=9727), _lib.KRK_ERR_INVALID, "even N"),
+    (dict(x=0), _lib.KRK_ERR_INVALID, "null operand"),
+    (dict(y=0), _lib.KRK_ERR_INVALID, "null operand"),
+    (dict(ldx=2552), _lib.KRK_ERR_INVALID, "ldx"),
+    (dict(ldy=100), _lib.KRK_ERR_INVALID, "ldy"),
+    (dict(ldx=2561), _lib.KRK_ERR_ALIGN, "multiples of 8"),
+    (dict(x=X + 8), _lib.KRK_ERR_ALIGN, "16-byte aligned"),
+    (dict(w=W + 2), _lib.KRK_ERR_ALIGN, "16-byte aligned"),
+    (dict(y=Y + 1), _lib.KRK_ERR_ALIGN, "2-byte aligned"),
+    (dict(y=X + 1024), _lib.KRK_ERR_ALIAS, "may not share"),
+    (dict(y=W + 4096), _lib.KRK_ERR_ALIAS, "may not share"),
+])
+def test_argument_errors(lib, kw, code, msg):
+    assert call(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def _split_shape(lib):
+    """A shape whose plan splits K (o_proj at M = 1) and its workspace size."""
+    M, N, K = 1, 2560, 4096
+    need = lib.krk_gemm_workspace_bytes(M, N, K, NONE)
+    assert need > 0
+    return M, N, K, need
+
+
+def test_workspace_errors(lib):
+    M, N, K, need = _split_shape(lib)
+    kw = dict(M=M, N=N, K=K, ldx=K, ldw=K)
+    assert call(lib, **kw) == _lib.KRK_ERR_WORKSPACE and "needs a" in _lib.last_error()
+    assert call(lib, ws=WS, wsb=need - 1, **kw) == _lib.KRK_ERR_WORKSPACE
+    assert call(lib, ws=WS + 4, wsb=need, **kw) == _lib.KRK_ERR_ALIGN
+    assert call(lib, ws=Y, wsb=need, **kw) == _lib.KRK_ERR_ALIAS
+
+
+def test_workspace_size_formula(lib):
+    for M, N, K, epi in [(1, 2560, 4096, NONE), (4, 2560, 9728, NONE), (64, 2560, 9728, NONE),
+                         (1, 6144, 2560, NONE), (8, 19456, 2560, SILU), (200, 2560, 9728, NONE)]:
+        cfg = GemmConfig()
+        assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
+        got = lib.krk_gemm_workspace_bytes(M, N, K, epi)
+        if cfg.splits == 1:
+            assert got == 0
+            continue
+        nout = N // 2 if epi == SILU else N
+        cb = 16 * (cfg.n_tiles // 2 if epi == SILU else cfg.n_tiles)
+        nblocks = -(-nout // cb)
+        ctr = -(-nblocks * 4 // 256) * 256
+        assert got == ctr + cfg.splits * min(M, 64) * N * 4
+
+
+def test_workspace_bytes_invalid_shape_is_zero(lib):
+    assert lib.krk_gemm_workspace_bytes(0, 10, 16, NONE) == 0
+    assert lib.krk_gemm_workspace_bytes(1, 10, 12, NONE) == 0
+    assert lib.krk_gemm_workspace_bytes(1, 11, 16, SILU) == 0
+
+
+QWEN = {"qkv": (6144, 2560, NONE), "o": (2560, 4096, NONE), "gate_up": (19456, 2560, SILU),
+        "down": (2560, 9728, NONE), "lm_head": (151936, 2560, NONE)}
+
+
+@pytest.mark.parametrize("shape", sorted(QWEN))
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 32, 64])
+def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
+    N, K, epi = QWEN[shape]
+    cfg = GemmConfig()
+    assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
+    c = cfg.as_dict()
+    if c["kernel"] == _lib.KERNEL_MFMA:
+        assert 16 * c["m_tiles"] >= M
+        nout = N // 2 if epi == SILU else N
+        cb = 16 * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
+        blocks = -(-nout // cb) * c["splits"]
+        assert blocks >= 256, f"{shape} M={M}: {blocks} workgroups cannot fill 256 CUs ({c})"
+    assert c["splits"] >= 1 and c["waves"] >= 1
+
+
+@pytest.mark.parametrize("cfg,code,msg", [
+    (dict(kernel=9), _lib.KRK_ERR_UNSUPPORTED, "unknown kernel"),
+    (dict(kernel=1, m_tiles=1), _lib.KRK_ERR_INVALID, "cannot cover"),
+    (dict(kernel=1, n_tiles=3), _lib.KRK_ERR_UNSUPPORTED, "n_tiles"),
+    (dict(kernel=1, unroll=3), _lib.KRK_ERR_UNSUPPORTED, "unroll"),
+    (dict(kernel=1, waves=8), _lib.KRK_ERR_UNSUPPORTED, "waves"),
+    (dict(kernel=1, splits=33), _lib.KRK_ERR_UNSUPPORTED, "splits"),
+    (dict(kernel=2), _lib.KRK_ERR_UNSUPPORTED, "VALU"),
+])
+def test_config_errors(lib, cfg, code, msg):
+    c = GemmConfig.from_dict(cfg)
+    rc = lib.krk_gemm_bf16_config(X, 2560, W, 2560, Y, 6144, 20, 6144, 2560, NONE, ctypes.byref(c), 0, 0, None)
+    assert rc == code
+    assert msg in _lib.last_error()
+
+
+def test_silu_needs_even_tiles(lib):
+    c = GemmConfig.from_dict(dict(kernel=1, n_tiles=1))
+    rc = lib.krk_gemm_bf16_config(X, 2560, W, 2560, Y, 9728, 1, 19456, 2560, SILU, ctypes.byref(c), 0, 0, None)
+    assert rc == _lib.KRK_ERR_UNSUPPORTED and "even n_tiles" in _lib.last_error()
+
+
+def test_last_error_is_cleared_by_a_plan_call(lib):
+    call(lib, M=0)
+    assert _lib.last_error()
+    cfg = GemmConfig()
+    assert lib.krk_gemm_plan(1, 6144, 2560, NONE, ctypes.byref(cfg)) == 0
+    assert _lib.last_error() == ""
+
+
+def test_python_wrapper_rejects_cpu_and_bad_tensors():
+    import torch
+
+    from kernels.gemm import gemm_into
+
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    w = torch.zeros(32, 64, dtype=torch.bfloat16)
+    y = torch.zeros(2, 32, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        gemm_into(x, w, y)
+    with pytest.raises(ValueError, match="bfloat16"):
+        gemm_into(x.float(), w, y)
+    with pytest.raises(ValueError, match="contiguous"):
+        gemm_into(x.t().contiguous().t(), w, y)
+    with pytest.raises(ValueError, match="rows"):
+        gemm_into(x, w, y[:1])
+
+
+def test_error_mapping():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.KRK_ERR_ALIAS)
+    with pytest.raises(_lib.KrkError):
+        _lib.check(_lib.KRK_ERR_HIP)
+    _lib.check(_lib.KRK_OK)
