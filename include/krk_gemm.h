@@ -97,16 +97,20 @@ size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue);
 enum {
     KRK_KERNEL_AUTO = 0,
     KRK_KERNEL_MFMA = 1,   /* bf16 MFMA 16x16x32 tiles, W fragments straight from HBM */
-    KRK_KERNEL_VALU = 2    /* VALU dot2 row streaming, x staged in LDS (M <= 8) */
+    KRK_KERNEL_VALU = 2,   /* VALU dot2 row streaming, x staged in LDS (M <= 8) */
+    KRK_KERNEL_MFMA_LDS = 3, /* bf16 MFMA 16x16x32, W streamed row-contiguously through LDS */
+    KRK_KERNEL_STREAM = 5   /* persistent bf16 MFMA: W through an LDS DMA ring, x held in registers */
 };
 
 typedef struct krk_gemm_config {
     int kernel;   /* KRK_KERNEL_* */
-    int m_tiles;  /* MFMA: 16-row x tiles per wave, covering M (1..4); VALU: ignored */
-    int n_tiles;  /* MFMA: 16-row W tiles per wave (1, 2, 4; even with SILU_MUL);
-                     VALU: W rows per wave (1, 2, 4) */
-    int unroll;   /* k-steps loaded per pipeline stage (MFMA: 2, 4, 8; VALU: 1, 2, 4) */
-    int waves;    /* waves per workgroup (1, 2, 4, 8) */
+    int m_tiles;  /* MFMA kernels: 16-row x tiles covering M (1..4); VALU: ignored */
+    int n_tiles;  /* MFMA kernels: 16-row W tiles per workgroup (1, 2, 4; even with
+                     SILU_MUL); VALU: W rows per wave (1, 2, 4) */
+    int unroll;   /* k-steps loaded per pipeline stage (MFMA: 2, 4, 8; VALU: 1, 2, 4;
+                     MFMA_LDS: ignored, a stage is 512 k); STREAM: ring depth in
+                     512-k stages (2..8) */
+    int waves;    /* waves per workgroup (1, 2, 4; MFMA_LDS: 4; STREAM: 8, n_tiles 1) */
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
 } krk_gemm_config;
 

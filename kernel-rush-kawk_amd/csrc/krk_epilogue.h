@@ -7,16 +7,43 @@
 //   * every workgroup (block b, split s) writes its fp32 sums to
 //     part[s][m][col] (col indexes W rows: gate cols [0, Nout), up cols
 //     [Nout, N) for SILU_MUL);
-//   * it then releases (agent-scope fence) and bumps the block's counter;
-//   * the workgroup that sees the count reach splits-1 acquires, sums the
-//     partials in the fixed order s = 0, 1, ..., splits-1 (so the result does
-//     not depend on which split finished last), applies the epilogue, stores
-//     y and resets the counter to zero for the next call.
+//   * it waits for those stores to complete and bumps the block's counter;
+//   * the workgroup that sees the count reach splits-1 sums the partials in
+//     the fixed order s = 0, 1, ..., splits-1 (so the result does not depend
+//     on which split finished last), applies the epilogue, stores y and resets
+//     the counter to zero for the next call.
+//
+// Coherence.  The workgroups of one block run on different XCDs, whose L2
+// caches are not coherent with each other.  An agent-scope fence
+// (__threadfence) makes plain stores visible by writing back and invalidating
+// the whole L2 (buffer_wbl2 sc1 / buffer_inv sc1), which costs tens of
+// microseconds over a few hundred workgroups.  Instead every access to the
+// shared partials is an agent-scope atomic (global_store/global_load with sc1,
+// coherent across XCDs on its own), and the only ordering needed — partials
+// complete before the counter moves, partial reads after the counter is seen
+// — is enforced by s_waitcnt vmcnt(0) before the counter update and by the
+// counter's returned value gating the reads.  This is the agent-scope
+// release/acquire sequence of the gfx942/gfx950 memory model without the
+// L2 maintenance that only non-atomic accesses require.
 #pragma once
 
 #include "krk_common.h"
 
 namespace krk {
+
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this wave issued has completed; the
+// signal fences keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void drain_memory() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 template <bool SILU>
 struct OutStage {
@@ -33,8 +60,8 @@ struct OutStage {
             y[(int64_t)m * ldy + c] = (uint16_t)v;
         } else {
             float* p = part + ((int64_t)s * M + m) * N;
-            p[c] = g;
-            if (SILU) p[Nout + c] = u;
+            store_agent(p + c, g);
+            if (SILU) store_agent(p + Nout + c, u);
         }
     }
 };
@@ -45,26 +72,25 @@ template <bool SILU>
 __device__ void splitk_finish(const OutStage<SILU>& o, uint32_t* __restrict__ ctr,
                               int blk, int c0, int cb) {
     __shared__ int is_last;
-    __threadfence();
+    drain_memory();
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(ctr + blk, 1u);
+        const uint32_t prev = __hip_atomic_fetch_add(ctr + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = (prev == (uint32_t)(o.splits - 1));
     }
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     const int n = cb < o.Nout - c0 ? cb : o.Nout - c0;
     const int64_t sstride = (int64_t)o.M * o.N;
     for (int e = threadIdx.x; e < o.M * n; e += blockDim.x) {
         const int m = e / n;
         const int c = c0 + (e - m * n);
         const float* p = o.part + (int64_t)m * o.N + c;
-        float g = p[0];
-        float u = SILU ? p[o.Nout] : 0.0f;
+        float g = load_agent(p);
+        float u = SILU ? load_agent(p + o.Nout) : 0.0f;
         for (int s = 1; s < o.splits; ++s) {
-            g += p[s * sstride];
-            if (SILU) u += p[s * sstride + o.Nout];
+            g += load_agent(p + s * sstride);
+            if (SILU) u += load_agent(p + s * sstride + o.Nout);
         }
         const uint32_t v = SILU ? silu_mul_bf16(g, u) : f32_to_bf16(g);
         o.y[(int64_t)m * o.ldy + c] = (uint16_t)v;

@@ -14,6 +14,8 @@
 
 #include "krk_gemm.h"
 #include "krk_mfma.h"
+#include "krk_mfma_lds.h"
+#include "krk_stream.h"
 
 namespace {
 
@@ -63,6 +65,8 @@ Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
     g.Nout = silu ? N / 2 : N;
     if (c.kernel == KRK_KERNEL_VALU) {
         g.cb = c.waves * c.n_tiles;  // one group of n_tiles channels per wave
+    } else if (c.kernel == KRK_KERNEL_STREAM) {
+        g.cb = silu ? 8 : 16;  // one 16-row tile: 16 channels, or 8 gate + 8 up rows
     } else {
         g.cb = 16 * (silu ? c.n_tiles / 2 : c.n_tiles);
     }
@@ -71,27 +75,110 @@ Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
 }
 
 // The dispatch table.  Every projection is HBM-bound (arithmetic intensity is
-// about M flop/byte); the table only decides how the weight stream is cut so
-// all 256 CUs stream from the first cycle.
+// about M flop/byte), so the table only decides how the weight stream is cut.
+// Entries for the five Qwen3-4B projections were chosen by timing every
+// configuration on an MI355X (graph replay over 24 distinct weight copies);
+// other shapes use the rule in auto_config below.
+struct TableEntry {
+    int N, K, epilogue, m_lo, m_hi;
+    krk_gemm_config cfg;  // m_tiles 0: derived from M
+};
+constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits) {
+    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits};
+}
+const TableEntry kTable[] = {
+    // qkv 2560 -> 6144
+    {6144, 2560, KRK_EPILOGUE_NONE, 1, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    // o_proj 4096 -> 2560
+    {2560, 4096, KRK_EPILOGUE_NONE, 1, 8, kcfg(KRK_KERNEL_MFMA, 1, 4, 4, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 9, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 25, 32, kcfg(KRK_KERNEL_MFMA_LDS, 1, 0, 0, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 2)},
+    // gate_up 2560 -> 2 x 9728 with SiLU*mul
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 25, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    // down 9728 -> 2560
+    {2560, 9728, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 4)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 5, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
+    // lm_head 2560 -> 151936
+    {151936, 2560, KRK_EPILOGUE_NONE, 1, 8, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 4, 0, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
+};
+
+int stream_xs(int MT, int nst);
+
 void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
+    const int mt = cdiv(Mc, 16);
+    for (const TableEntry& e : kTable) {
+        if (e.N == N && e.K == K && e.epilogue == epilogue && Mc >= e.m_lo && Mc <= e.m_hi) {
+            *c = e.cfg;
+            c->m_tiles = mt;
+            if (c->kernel == KRK_KERNEL_MFMA_LDS) c->waves = 4, c->unroll = 1;
+            if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
+            return;
+        }
+    }
+    // Other shapes: the persistent stream kernel where x is large and the
+    // weight stream long (its x-in-registers design pays off), otherwise the
+    // LDS-staged MFMA kernel with K split until ~200 workgroups stream.
     const int Nout = silu ? N / 2 : N;
-    const int KS = cdiv(K, 32);
+    const int KST = cdiv(K, 512);
     krk_gemm_config r{};
-    r.kernel = KRK_KERNEL_MFMA;
-    r.m_tiles = cdiv(Mc, 16);
-    r.n_tiles = silu ? 2 : (Mc <= 16 ? 1 : 2);
-    r.unroll = r.m_tiles == 1 ? 8 : 4;
-    r.waves = 4;
-    const int cb = 16 * (silu ? r.n_tiles / 2 : r.n_tiles);
-    const int nblocks = cdiv(Nout, cb);
-    int splits = 1;
-    while (nblocks * splits < 2 * kCuCount && splits < 8 &&
-           KS / (2 * splits * r.waves) >= r.unroll)
-        splits *= 2;
-    r.splits = splits;
+    r.m_tiles = mt;
+    if (Mc > 32 && (silu || N >= 65536)) {
+        r.kernel = KRK_KERNEL_STREAM;
+        r.n_tiles = 1;
+        r.waves = 8;
+        r.unroll = 4;
+        r.splits = 1;
+        while (r.splits < 32 && stream_xs(mt, cdiv(KST, r.splits)) == 0) ++r.splits;
+    } else {
+        r.kernel = KRK_KERNEL_MFMA_LDS;
+        r.n_tiles = (N >= 65536 && Mc > 8) ? 4 : 2;
+        r.unroll = 1;
+        r.waves = 4;
+        const int nblocks = cdiv(Nout, 16 * (silu ? r.n_tiles / 2 : r.n_tiles));
+        r.splits = 1;
+        while (nblocks * r.splits < 192 && r.splits < 4 && KST >= 2 * (r.splits + 1)) ++r.splits;
+    }
     *c = r;
+}
+
+// Dynamic LDS a gfx950 workgroup may use: 160 KB less room for the kernels'
+// static __shared__ variables.
+constexpr size_t kLdsMax = 163840 - kLdsReserve;
+
+// STREAM: x fragments live in 8·XS·MT VGPRs per lane; the instantiated XS
+// values per MT are the ones that stay within 256 VGPRs without spilling in
+// the stage loop (MT=4, XS=5 spills a few bytes outside it).
+int stream_xs(int MT, int nst) {
+    static const int kXs[4][4] = {{4, 5, 8, 10}, {4, 5, 8, 0}, {4, 5, 0, 0}, {4, 5, 0, 0}};
+    for (int xs : kXs[MT - 1])
+        if (xs && xs >= nst) return xs;
+    return 0;
+}
+inline int stream_max_depth(int MT) {
+    int d = krk::kStreamMaxDepth;
+    while (d > 2 && krk::stream_lds_bytes(MT, d) > kLdsMax) --d;
+    return d;
+}
+// Persistent grid: workgroups per split, at most one per CU, chosen so the
+// blocks divide as evenly as possible (a 1.25x overload costs more than
+// leaving CUs idle).
+inline int stream_groups(int nblocks, int splits) {
+    const int cap = kCuCount / splits > 0 ? kCuCount / splits : 1;
+    if (nblocks <= cap) return nblocks;
+    int best = cap;
+    double best_eff = 0.0;
+    for (int g = cap; g >= cap / 2 && g >= 1; --g) {
+        const int per = cdiv(nblocks, g);
+        const double eff = (double)nblocks / ((double)per * kCuCount / splits);
+        if (eff > best_eff + 1e-9) { best_eff = eff; best = g; }
+    }
+    return best;
 }
 
 // Fill the zero fields of a caller's configuration from the table and check
@@ -121,6 +208,38 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
         if (c.waves > 0 && (size_t)c.waves * c.m_tiles * c.n_tiles * 1024 + kLdsReserve > kLdsBudget)
             return fail(KRK_ERR_UNSUPPORTED, "waves*m_tiles*n_tiles=%d KB of reduction LDS exceeds the %zu-byte budget",
                         c.waves * c.m_tiles * c.n_tiles, kLdsBudget);
+    } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {
+        if (!c.m_tiles) c.m_tiles = cdiv(Mc, 16);
+        if (!c.n_tiles) c.n_tiles = same_kernel ? a.n_tiles : (epilogue == KRK_EPILOGUE_SILU_MUL ? 2 : 1);
+        if (!c.unroll) c.unroll = 1;
+        if (!c.waves) c.waves = krk::kLdsWaves;
+        if (!c.splits) c.splits = same_kernel ? a.splits : 1;
+        if (c.m_tiles < cdiv(Mc, 16) || c.m_tiles > 4)
+            return fail(KRK_ERR_INVALID, "m_tiles=%d cannot cover %d rows (need %d..4)", c.m_tiles, Mc, cdiv(Mc, 16));
+        if (c.n_tiles != 1 && c.n_tiles != 2 && c.n_tiles != 4)
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS n_tiles=%d not in {1,2,4}", c.n_tiles);
+        if (epilogue == KRK_EPILOGUE_SILU_MUL && c.n_tiles % 2)
+            return fail(KRK_ERR_UNSUPPORTED, "SILU_MUL needs an even n_tiles, got %d", c.n_tiles);
+        if (c.waves != krk::kLdsWaves)
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS runs %d waves per workgroup, got waves=%d", krk::kLdsWaves, c.waves);
+    } else if (c.kernel == KRK_KERNEL_STREAM) {
+        if (!c.m_tiles) c.m_tiles = cdiv(Mc, 16);
+        c.n_tiles = 1;
+        c.waves = krk::kStreamWaves;
+        if (!c.splits) c.splits = same_kernel ? a.splits : 1;
+        if (c.m_tiles < cdiv(Mc, 16) || c.m_tiles > 4)
+            return fail(KRK_ERR_INVALID, "m_tiles=%d cannot cover %d rows (need %d..4)", c.m_tiles, Mc, cdiv(Mc, 16));
+        if (c.splits < 1 || c.splits > 32)
+            return fail(KRK_ERR_UNSUPPORTED, "splits=%d not in 1..32", c.splits);
+        if (stream_xs(c.m_tiles, cdiv(cdiv(K, krk::kStreamKC), c.splits)) == 0)
+            return fail(KRK_ERR_UNSUPPORTED, "STREAM keeps x in registers: %d K stages per split x %d m tiles is too "
+                        "many (raise splits)", cdiv(cdiv(K, krk::kStreamKC), c.splits), c.m_tiles);
+        const int maxd = stream_max_depth(c.m_tiles);
+        if (!c.unroll) c.unroll = same_kernel && a.unroll ? a.unroll : maxd;
+        if (c.unroll < 2 || c.unroll > maxd)
+            return fail(KRK_ERR_UNSUPPORTED, "STREAM depth (unroll) %d not in 2..%d", c.unroll, maxd);
+        *out = c;
+        return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_VALU) {
         if (Mc > kValuMaxRows)
             return fail(KRK_ERR_UNSUPPORTED, "VALU kernel handles M <= %d, got %d", kValuMaxRows, M);
@@ -212,6 +331,93 @@ int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
 }
 
+template <int MT, int NT, bool SILU>
+int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, SILU>);
+    const size_t shm = krk::mfma_lds_bytes(MT, NT);
+    // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once per
+    // instantiation (a function attribute, not a stream operation).
+    static const hipError_t attr = shm > 65536 ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm)
+                                               : hipSuccess;
+    if (attr != hipSuccess) return hip_status(attr, "mfma_lds_kernel LDS attribute");
+    void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
+                    (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr};
+    hipError_t e = hipLaunchKernel(fn, dim3(nblocks * a.splits), dim3(64 * krk::kLdsWaves), args, shm, stream);
+    return hip_status(e, "mfma_lds_kernel launch");
+}
+
+template <int MT, bool SILU>
+int dispatch_mfma_lds_n(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    if constexpr (!SILU) {
+        if (c.n_tiles == 1) return launch_mfma_lds<MT, 1, false>(a, nblocks, s);
+    }
+    if (c.n_tiles == 2) return launch_mfma_lds<MT, 2, SILU>(a, nblocks, s);
+    if (c.n_tiles == 4) return launch_mfma_lds<MT, 4, SILU>(a, nblocks, s);
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS n_tiles=%d", c.n_tiles);
+}
+
+template <bool SILU>
+int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    switch (c.m_tiles) {
+        case 1: return dispatch_mfma_lds_n<1, SILU>(a, c, nblocks, s);
+        case 2: return dispatch_mfma_lds_n<2, SILU>(a, c, nblocks, s);
+        case 3: return dispatch_mfma_lds_n<3, SILU>(a, c, nblocks, s);
+        case 4: return dispatch_mfma_lds_n<4, SILU>(a, c, nblocks, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
+}
+
+template <int MT, int XS, bool SILU>
+int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU>);
+    const size_t shm = krk::stream_lds_bytes(MT, depth);
+    if (shm > kLdsMax) return fail(KRK_ERR_UNSUPPORTED, "STREAM needs %zu bytes of LDS", shm);
+    static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    if (attr != hipSuccess) return hip_status(attr, "stream_gemm_kernel LDS attribute");
+    const int groups = stream_groups(nblocks, a.splits) * a.splits;
+    void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
+                    (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth,
+                    (void*)&a.part, (void*)&a.ctr};
+    hipError_t e = hipLaunchKernel(fn, dim3(groups), dim3(64 * krk::kStreamWaves), args, shm, stream);
+    return hip_status(e, "stream_gemm_kernel launch");
+}
+
+template <int MT, bool SILU>
+int dispatch_stream_xs(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    const int xs = stream_xs(MT, cdiv(cdiv(a.K, krk::kStreamKC), c.splits));
+    if constexpr (MT == 1) {
+        switch (xs) {
+            case 4: return launch_stream<1, 4, SILU>(a, nblocks, c.unroll, s);
+            case 5: return launch_stream<1, 5, SILU>(a, nblocks, c.unroll, s);
+            case 8: return launch_stream<1, 8, SILU>(a, nblocks, c.unroll, s);
+            case 10: return launch_stream<1, 10, SILU>(a, nblocks, c.unroll, s);
+        }
+    } else if constexpr (MT == 2) {
+        switch (xs) {
+            case 4: return launch_stream<2, 4, SILU>(a, nblocks, c.unroll, s);
+            case 5: return launch_stream<2, 5, SILU>(a, nblocks, c.unroll, s);
+            case 8: return launch_stream<2, 8, SILU>(a, nblocks, c.unroll, s);
+        }
+    } else {
+        switch (xs) {
+            case 4: return launch_stream<MT, 4, SILU>(a, nblocks, c.unroll, s);
+            case 5: return launch_stream<MT, 5, SILU>(a, nblocks, c.unroll, s);
+        }
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "STREAM has no x-register layout for m_tiles=%d and this K split", MT);
+}
+
+template <bool SILU>
+int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    switch (c.m_tiles) {
+        case 1: return dispatch_stream_xs<1, SILU>(a, c, nblocks, s);
+        case 2: return dispatch_stream_xs<2, SILU>(a, c, nblocks, s);
+        case 3: return dispatch_stream_xs<3, SILU>(a, c, nblocks, s);
+        case 4: return dispatch_stream_xs<4, SILU>(a, c, nblocks, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
+}
+
 template <bool SILU>
 int dispatch_valu(const LaunchArgs&, const krk_gemm_config&, int, hipStream_t) {
     return fail(KRK_ERR_UNSUPPORTED, "VALU kernel not built yet");
@@ -274,6 +480,10 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
         a.ctr = ctr;
         if (c.kernel == KRK_KERNEL_MFMA) {
             rc = silu ? dispatch_mfma<true>(a, c, g.nblocks, st) : dispatch_mfma<false>(a, c, g.nblocks, st);
+        } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {
+            rc = silu ? dispatch_mfma_lds<true>(a, c, g.nblocks, st) : dispatch_mfma_lds<false>(a, c, g.nblocks, st);
+        } else if (c.kernel == KRK_KERNEL_STREAM) {
+            rc = silu ? dispatch_stream<true>(a, c, g.nblocks, st) : dispatch_stream<false>(a, c, g.nblocks, st);
         } else {
             rc = silu ? dispatch_valu<true>(a, c, g.nblocks, st) : dispatch_valu<false>(a, c, g.nblocks, st);
         }

@@ -18,17 +18,71 @@
 //     so the epilogue pairs stay in registers) and one of `splits` K ranges;
 //   * its waves divide that K range again (32-wide k-steps) and stream their
 //     W slice with non-temporal 16-byte loads, U k-steps per pipeline stage,
-//     double-buffered in registers so a stage is in flight while the
+//     double-buffered in registers so one stage is in flight while the
 //     previous one feeds the MFMAs;
 //   * x fragments come straight from global memory: x is at most 64 x K bf16
-//     and stays resident in L2 while W streams past it;
+//     and stays resident in L1/L2 while W streams past it;
 //   * waves are reduced in a fixed order through LDS, then OutStage stores y
 //     (splits == 1) or the fp32 partials that splitk_finish reduces.
+//
+// The main loop is branch-free: rows past M (x) or N (W) load a clamped, valid
+// row and are zeroed by a select or never stored, and the prefetch of the
+// next stage is unconditional (the last stage is peeled), so the compiler can
+// wait for exactly one stage's loads at a time.  K tails (K % 32 != 0) go
+// through a separate masked single-step path.
 #pragma once
 
 #include "krk_epilogue.h"
 
 namespace krk {
+
+template <int MT, int NT>
+struct MfmaFrag {
+    const uint16_t* wp[NT];
+    const uint16_t* xp[MT];
+    uint32_t xmask[MT];  // all-ones for rows < M, zero for padding rows
+
+    __device__ __forceinline__ void load_step(int koff, bf16x8 (&wr)[NT], bf16x8 (&xr)[MT]) const {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wr[t] = __builtin_bit_cast(bf16x8, load_stream16(wp[t] + koff));
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            u32x4 v = load_cached16(xp[i] + koff);
+            v &= xmask[i];
+            xr[i] = __builtin_bit_cast(bf16x8, v);
+        }
+    }
+
+    // One k-step at koff whose 8-element groups may run past K: groups at or
+    // past K load a valid in-range address and are zeroed.
+    __device__ __forceinline__ void load_step_tail(int koff, int q, int K, bf16x8 (&wr)[NT],
+                                                   bf16x8 (&xr)[MT]) const {
+        const bool ok = koff + 8 * q < K;
+        const int kk = ok ? koff : K - 8 - 8 * q;  // stays inside the row
+        const uint32_t m = ok ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            u32x4 v = load_stream16(wp[t] + kk);
+            v &= m;
+            wr[t] = __builtin_bit_cast(bf16x8, v);
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            u32x4 v = load_cached16(xp[i] + kk);
+            v &= (xmask[i] & m);
+            xr[i] = __builtin_bit_cast(bf16x8, v);
+        }
+    }
+};
+
+template <int MT, int NT>
+__device__ __forceinline__ void mma_step(f32x4 (&acc)[MT][NT], const bf16x8 (&wr)[NT], const bf16x8 (&xr)[MT]) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xr[i], wr[t], acc[i][t], 0, 0, 0);
+}
 
 template <int MT, int NT, int U, bool SILU>
 __global__ void __launch_bounds__(256)
@@ -53,23 +107,19 @@ mfma_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int Nout = SILU ? (N >> 1) : N;
     const int c0 = blk * (16 * NH);
 
-    // Row pointers.  Rows past the end are clamped to a valid row; their
-    // results are never stored.
-    const uint16_t* wp[NT];
+    MfmaFrag<MT, NT> f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         int ch = c0 + 16 * (t % NH) + r;
         ch = ch < Nout ? ch : Nout - 1;
         const int row = (SILU && t >= NH) ? ch + Nout : ch;
-        wp[t] = w + (int64_t)row * ldw + 8 * q;
+        f.wp[t] = w + (int64_t)row * ldw + 8 * q;
     }
-    const uint16_t* xp[MT];
-    bool xv[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         const int m = 16 * i + r;
-        xv[i] = m < M;
-        xp[i] = x + (int64_t)(xv[i] ? m : 0) * ldx + 8 * q;
+        f.xmask[i] = m < M ? 0xffffffffu : 0u;
+        f.xp[i] = x + (int64_t)(m < M ? m : M - 1) * ldx + 8 * q;
     }
 
     // This wave's k-steps [kb, ke) (32 elements each).
@@ -77,8 +127,9 @@ mfma_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int P = splits * waves;
     const int j = s * waves + wave;
     const int kb = (int)(((int64_t)j * KS) / P);
-    const int ke = (int)(((int64_t)(j + 1) * KS) / P);
-    const bool kfull = (K & 31) == 0;
+    int ke = (int)(((int64_t)(j + 1) * KS) / P);
+    const bool tail = (K & 31) && ke == KS;  // this wave owns the ragged last step
+    if (tail) --ke;
 
     f32x4 acc[MT][NT];
 #pragma unroll
@@ -88,68 +139,48 @@ mfma_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
     bf16x8 wa[U][NT], xa[U][MT];
     bf16x8 wb[U][NT], xb[U][MT];
-
-    // Load the U k-steps starting at g into (wr, xr).  Steps at or past ke and
-    // k positions at or past K load zeros.
     auto load_stage = [&](int g, bf16x8 (&wr)[U][NT], bf16x8 (&xr)[U][MT]) {
-        if (g + U <= ke && kfull) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int koff = (g + u) << 5;
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    wr[u][t] = __builtin_bit_cast(bf16x8, load_stream16(wp[t] + koff));
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    u32x4 v = {0u, 0u, 0u, 0u};
-                    if (xv[i]) v = load_cached16(xp[i] + koff);
-                    xr[u][i] = __builtin_bit_cast(bf16x8, v);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int koff = (g + u) << 5;
-                const bool ok = (g + u) < ke && (koff + 8 * q) < K;
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    u32x4 v = {0u, 0u, 0u, 0u};
-                    if (ok) v = load_stream16(wp[t] + koff);
-                    wr[u][t] = __builtin_bit_cast(bf16x8, v);
-                }
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    u32x4 v = {0u, 0u, 0u, 0u};
-                    if (ok && xv[i]) v = load_cached16(xp[i] + koff);
-                    xr[u][i] = __builtin_bit_cast(bf16x8, v);
-                }
-            }
-        }
+        for (int u = 0; u < U; ++u) f.load_step((g + u) << 5, wr[u], xr[u]);
     };
-
     auto mma_stage = [&](const bf16x8 (&wr)[U][NT], const bf16x8 (&xr)[U][MT]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xr[u][i], wr[u][t],
-                                                                         acc[i][t], 0, 0, 0);
+        for (int u = 0; u < U; ++u) mma_step<MT, NT>(acc, wr[u], xr[u]);
     };
 
-    // Two-stage register pipeline, unrolled by two so the buffers swap roles
-    // without register copies.
+    // Full stages, double-buffered; the last stage is peeled so every
+    // in-loop prefetch is unconditional.
+    const int nst = (ke - kb) / U;
     int g = kb;
-    if (g < ke) load_stage(g, wa, xa);
-    while (g < ke) {
-        if (g + U < ke) load_stage(g + U, wb, xb);
-        mma_stage(wa, xa);
-        g += U;
-        if (g >= ke) break;
-        if (g + U < ke) load_stage(g + U, wa, xa);
-        mma_stage(wb, xb);
-        g += U;
+    if (nst > 0) {
+        load_stage(g, wa, xa);
+        int left = nst - 1;  // stages still to load
+        while (left >= 2) {
+            load_stage(g + U, wb, xb);
+            mma_stage(wa, xa);
+            load_stage(g + 2 * U, wa, xa);
+            mma_stage(wb, xb);
+            g += 2 * U;
+            left -= 2;
+        }
+        if (left == 1) {
+            load_stage(g + U, wb, xb);
+            mma_stage(wa, xa);
+            mma_stage(wb, xb);
+            g += 2 * U;
+        } else {
+            mma_stage(wa, xa);
+            g += U;
+        }
+    }
+    // Remaining whole steps, one at a time.
+    for (; g < ke; ++g) {
+        f.load_step(g << 5, wa[0], xa[0]);
+        mma_step<MT, NT>(acc, wa[0], xa[0]);
+    }
+    if (tail) {
+        f.load_step_tail(ke << 5, q, K, wa[0], xa[0]);
+        mma_step<MT, NT>(acc, wa[0], xa[0]);
     }
 
     // Cross-wave reduction in fixed wave order.

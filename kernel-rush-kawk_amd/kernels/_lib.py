@@ -30,6 +30,8 @@ EPILOGUE_SILU_MUL = 1
 KERNEL_AUTO = 0
 KERNEL_MFMA = 1
 KERNEL_VALU = 2
+KERNEL_MFMA_LDS = 3
+KERNEL_STREAM = 5
 
 #: Every function the header declares, with (restype, argtypes).
 _c_void_p = ctypes.c_void_p

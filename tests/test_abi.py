@@ -71,11 +71,19 @@ def test_argument_errors(lib, kw, code, msg):
 
 
 def _split_shape(lib):
-    """A shape whose plan splits K (o_proj at M = 1) and its workspace size."""
-    M, N, K = 1, 2560, 4096
+    """A shape whose plan splits K (down_proj at M = 1) and its workspace size."""
+    M, N, K = 1, 2560, 9728
+    cfg = GemmConfig()
+    assert lib.krk_gemm_plan(M, N, K, NONE, ctypes.byref(cfg)) == 0 and cfg.splits > 1
     need = lib.krk_gemm_workspace_bytes(M, N, K, NONE)
     assert need > 0
     return M, N, K, need
+
+
+def _channels_per_block(c, epi):
+    if c["kernel"] == _lib.KERNEL_STREAM:
+        return 8 if epi == SILU else 16
+    return 16 * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
 
 
 def test_workspace_errors(lib):
@@ -89,7 +97,8 @@ def test_workspace_errors(lib):
 
 def test_workspace_size_formula(lib):
     for M, N, K, epi in [(1, 2560, 4096, NONE), (4, 2560, 9728, NONE), (64, 2560, 9728, NONE),
-                         (1, 6144, 2560, NONE), (8, 19456, 2560, SILU), (200, 2560, 9728, NONE)]:
+                         (1, 6144, 2560, NONE), (8, 19456, 2560, SILU), (200, 2560, 9728, NONE),
+                         (40, 3000, 5000, SILU), (64, 100000, 3000, NONE)]:
         cfg = GemmConfig()
         assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
         got = lib.krk_gemm_workspace_bytes(M, N, K, epi)
@@ -97,8 +106,7 @@ def test_workspace_size_formula(lib):
             assert got == 0
             continue
         nout = N // 2 if epi == SILU else N
-        cb = 16 * (cfg.n_tiles // 2 if epi == SILU else cfg.n_tiles)
-        nblocks = -(-nout // cb)
+        nblocks = -(-nout // _channels_per_block(cfg.as_dict(), epi))
         ctr = -(-nblocks * 4 // 256) * 256
         assert got == ctr + cfg.splits * min(M, 64) * N * 4
 
@@ -113,20 +121,23 @@ QWEN = {"qkv": (6144, 2560, NONE), "o": (2560, 4096, NONE), "gate_up": (19456, 2
         "down": (2560, 9728, NONE), "lm_head": (151936, 2560, NONE)}
 
 
-@pytest.mark.parametrize("shape", sorted(QWEN))
-@pytest.mark.parametrize("M", [1, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("shape", sorted(QWEN) + ["other_silu", "other_wide"])
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 17, 32, 33, 48, 64, 100])
 def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
-    N, K, epi = QWEN[shape]
+    """Every plan covers the rows, and streams from enough CUs: >= 150
+    workgroups (measured: 160 one-per-CU workgroups stream a narrow shape at
+    ~95% of the 256-workgroup rate), or the persistent stream kernel."""
+    N, K, epi = QWEN.get(shape) or {"other_silu": (3000, 5000, SILU), "other_wide": (100000, 3000, NONE)}[shape]
     cfg = GemmConfig()
     assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
     c = cfg.as_dict()
-    if c["kernel"] == _lib.KERNEL_MFMA:
-        assert 16 * c["m_tiles"] >= M
-        nout = N // 2 if epi == SILU else N
-        cb = 16 * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
-        blocks = -(-nout // cb) * c["splits"]
-        assert blocks >= 256, f"{shape} M={M}: {blocks} workgroups cannot fill 256 CUs ({c})"
+    assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM)
+    assert 16 * c["m_tiles"] >= min(M, 64) and c["m_tiles"] <= 4
     assert c["splits"] >= 1 and c["waves"] >= 1
+    if c["kernel"] != _lib.KERNEL_STREAM:
+        nout = N // 2 if epi == SILU else N
+        blocks = -(-nout // _channels_per_block(c, epi)) * c["splits"]
+        assert blocks >= 150, f"{shape} M={M}: {blocks} workgroups ({c})"
 
 
 @pytest.mark.parametrize("cfg,code,msg", [

@@ -117,7 +117,7 @@ def test_c3_gateup_m8(device):
     check_gateup(x, w, "C3 gate_up+silu M=8")
 
 
-def _lm_argmax_check(x, lm, what):
+def _lm_argmax_check(x, lm, what, device):
     say(what, tuple(x.shape))
     logits = krk(x, lm)
     ref = R.linear_bf16(x, lm)
@@ -150,7 +150,7 @@ def lm_head():
 @pytest.mark.parametrize("M", [64, 32, 8, 1])
 def test_lm_head_argmax(device, lm_head, M):
     x = R.randn_bf16((M, R.HIDDEN), R.seed_for(5, M, "x"))
-    _lm_argmax_check(x, lm_head, f"lm_head M={M}")
+    _lm_argmax_check(x, lm_head, f"lm_head M={M}", device)
 
 
 @pytest.mark.parametrize("layer", [0, 17, 35])
@@ -215,7 +215,9 @@ def test_strided_operands(device):
     xd = big.to(device)[:, 32:32 + K]
     assert xd.stride(0) == K + 64
     ybig = torch.full((M, N + 24), 7.0, dtype=torch.bfloat16, device=device)
-    G.gemm_into(xd, w.to(device), ybig[:, 8:8 + N])
+    nbytes = G.workspace_bytes(M, N, K)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+    G.gemm_into(xd, w.to(device), ybig[:, 8:8 + N], NONE, ws)
     torch.cuda.synchronize()
     got = ybig.cpu()
     assert_parity(got[:, 8:8 + N], R.linear_bf16(big[:, 32:32 + K], w), "strided")
@@ -290,6 +292,74 @@ def test_all_mfma_gateup_configs_agree(device):
         assert_parity(krk(x, w, SILU, cfg), ref, f"gateup config {cfg}")
 
 
+def _lds_configs(M, silu):
+    mt_min = -(-min(M, 64) // 16)
+    for mt, nt, sp in itertools.product(range(mt_min, 5), (1, 2, 4), (1, 2, 3)):
+        if silu and nt % 2:
+            continue
+        yield dict(kernel=_lib.KERNEL_MFMA_LDS, m_tiles=mt, n_tiles=nt, splits=sp)
+
+
+def _stream_configs(M, K):
+    mt_min = -(-min(M, 64) // 16)
+    for mt, sp, d in itertools.product(range(mt_min, 5), (1, 2, 3), (2, 3, 5, 8)):
+        yield dict(kernel=_lib.KERNEL_STREAM, m_tiles=mt, splits=sp, unroll=d)
+
+
+def _run_configs(x, w, epi, configs):
+    """Run every configuration the library accepts; check each against the oracle."""
+    ref = R.gateup_bf16(x, w) if epi == SILU else R.linear_bf16(x, w)
+    bound = None if epi == SILU else R.linear_exact(x, w)
+    ran = 0
+    for cfg in configs:
+        if G.workspace_bytes(x.shape[0], w.shape[0], x.shape[1], epi, cfg) == 0 and cfg.get("splits", 1) > 1:
+            continue  # rejected configuration (e.g. x-register budget)
+        say("config", tuple(x.shape), tuple(w.shape), epi, cfg)
+        try:
+            y = krk(x, w, epi, cfg)
+        except ValueError as e:
+            if "krk error -6" in str(e):
+                continue
+            raise
+        assert_parity(y, ref, f"config {cfg}")
+        if bound is not None:
+            assert R.within_fp32_bound(y, bound[0], bound[1], x.shape[1]).all(), f"config {cfg}"
+        ran += 1
+    assert ran > 0
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 96, 1536), (13, 200, 1000), (40, 96, 2568), (64, 130, 520)])
+def test_all_lds_configs_agree(device, M, N, K):
+    x = R.randn_bf16((M, K), 8700 + M)
+    w = R.randn_bf16((N, K), 8701 + N, 0.02)
+    _run_configs(x, w, NONE, _lds_configs(M, False))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 96, 1536), (13, 200, 1000), (40, 96, 2568), (64, 130, 520), (5, 4099, 2048)])
+def test_all_stream_configs_agree(device, M, N, K):
+    x = R.randn_bf16((M, K), 8800 + M)
+    w = R.randn_bf16((N, K), 8801 + N, 0.02)
+    _run_configs(x, w, NONE, _stream_configs(M, K))
+
+
+@pytest.mark.parametrize("M,I,K", [(1, 40, 1536), (8, 52, 1000), (33, 24, 2568), (64, 100, 520)])
+def test_gateup_configs_all_kernels(device, M, I, K):
+    x = R.randn_bf16((M, K), 8900 + M)
+    w = R.randn_bf16((2 * I, K), 8901 + I, 0.02)
+    _run_configs(x, w, SILU, itertools.chain(_lds_configs(M, True), _stream_configs(M, K)))
+
+
+@pytest.mark.parametrize("M", [1, 8, 33, 64])
+def test_stream_persistent_many_blocks(device, M):
+    """More blocks than workgroups: every workgroup walks several blocks while
+    the ring streams across block boundaries (lm_head-like width)."""
+    K, N = 2560, 16 * 256 * 3 + 40
+    x = R.randn_bf16((M, K), 9000 + M)
+    w = R.randn_bf16((N, K), 9001, 0.02)
+    for cfg in (dict(kernel=_lib.KERNEL_STREAM, splits=1, unroll=4), dict(kernel=_lib.KERNEL_STREAM, splits=2, unroll=6)):
+        check_linear(x, w, f"stream persistent M={M}", cfg)
+
+
 def test_split_count_only_changes_summation_order(device):
     x = R.randn_bf16((1, 4096), 8300)
     w = R.randn_bf16((2560, 4096), 8301, 0.02)
@@ -312,7 +382,8 @@ def test_graph_capture_and_replay(device):
     """Calls (including split-K ones with their self-resetting counters) are
     captured in one graph and replayed several times, with eager work and
     synchronisation between replays; every replay matches the eager result."""
-    shapes = [(1, 6144, 2560, NONE), (1, 2560, 4096, NONE), (8, 19456, 2560, SILU), (64, 2560, 9728, NONE)]
+    shapes = [(1, 6144, 2560, NONE), (1, 2560, 4096, NONE), (8, 19456, 2560, SILU), (64, 2560, 9728, NONE),
+              (1, 2560, 9728, NONE), (48, 19456, 2560, SILU), (64, 20000, 2560, NONE)]
     mms, ins = [], []
     for i, (M, N, K, epi) in enumerate(shapes):
         cls = G.SkinnyGateUp(M, N // 2, K, device) if epi == SILU else G.SkinnyMatmul(M, N, K, device)
