@@ -40,6 +40,8 @@ SHAPES = {
     "lm_head": (HIDDEN, VOCAB, False),
 }
 TENSOR_ID = {"x": 0, "qkv": 1, "o": 2, "gate_up": 3, "down": 4, "lm_head": 5}
+# krk_gemm_config.kernel -> device function name (as rocprofv3 reports it)
+KERNEL_NAMES = {1: "mfma_gemm_kernel", 2: "valu_gemm_kernel", 3: "mfma_lds_kernel", 5: "stream_gemm_kernel"}
 
 
 def log(*a):
@@ -199,7 +201,8 @@ def main() -> int:
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": f"{dom} M={M} (mfma_gemm_kernel SILU)", "us_per_launch": round(dom_ms * 1000, 2),
+                "kernel": f"{dom} M={M} ({KERNEL_NAMES[ops[dom].resolved_config['kernel']]}, SiLU*mul)",
+                "config": ops[dom].resolved_config, "us_per_launch": round(dom_ms * 1000, 2),
                 "bytes_per_launch": dom_bytes}
     log(f"roofline {dom}: {dom_ms * 1000:.2f} us/launch, {achieved:.0f} GB/s")
 
@@ -251,7 +254,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) bf16 weights, random init)",
         "config": {"workload": f"C4 decode-step GEMM sweep, M={M}: 36 layers x {{qkv 2560->6144, o 4096->2560, "
-                               "gate_up 2560->19456 + SiLU*mul, down 9728->2560}} + lm_head 2560->151936, "
+                               "gate_up 2560->19456 + SiLU*mul, down 9728->2560} + lm_head 2560->151936, "
                                "distinct weights per layer", "M": M, "calls_per_step": 4 * LAYERS + 1,
                    "bytes_per_step": sweep_bytes, "graph": True},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),

@@ -16,6 +16,7 @@
 #include "krk_mfma.h"
 #include "krk_mfma_lds.h"
 #include "krk_stream.h"
+#include "krk_valu.h"
 
 namespace {
 
@@ -64,7 +65,7 @@ Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
     const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
     g.Nout = silu ? N / 2 : N;
     if (c.kernel == KRK_KERNEL_VALU) {
-        g.cb = c.waves * c.n_tiles;  // one group of n_tiles channels per wave
+        g.cb = c.waves * (silu ? c.n_tiles / 2 : c.n_tiles);  // n_tiles W rows per wave
     } else if (c.kernel == KRK_KERNEL_STREAM) {
         g.cb = silu ? 8 : 16;  // one 16-row tile: 16 channels, or 8 gate + 8 up rows
     } else {
@@ -86,25 +87,64 @@ struct TableEntry {
 constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits) {
     return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits};
 }
+// VALU entries: n_tiles = W rows per wave, unroll 0 = blocks in flight chosen
+// to cover a split's K range in one pass.
 const TableEntry kTable[] = {
     // qkv 2560 -> 6144
-    {6144, 2560, KRK_EPILOGUE_NONE, 1, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 3, 8, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 9, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
     // o_proj 4096 -> 2560
-    {2560, 4096, KRK_EPILOGUE_NONE, 1, 8, kcfg(KRK_KERNEL_MFMA, 1, 4, 4, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 9, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
     {2560, 4096, KRK_EPILOGUE_NONE, 25, 32, kcfg(KRK_KERNEL_MFMA_LDS, 1, 0, 0, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 2)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 25, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
-    {2560, 9728, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 4)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 5, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 2, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 9, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
     // lm_head 2560 -> 151936
-    {151936, 2560, KRK_EPILOGUE_NONE, 1, 8, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 4, 0, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
 };
+
+// VALU: x rows held per launch (a power of two >= M), and the instantiated
+// numbers of 512-element blocks in flight per W row.
+inline int valu_mx(int Mc) { return Mc <= 1 ? 1 : Mc <= 2 ? 2 : Mc <= 4 ? 4 : 8; }
+constexpr int kValuDepths[] = {2, 3, 4, 5, 7, 8, 10, 19};
+// Loads a lane keeps in flight: D blocks of R W rows, plus MX x rows when x
+// stays in registers (MX < 4).  48 keeps the kernels within 256 VGPRs.
+inline int valu_loads(int MX, int R, int D) { return (MX < krk::kValuLdsMinRows ? MX + R : R) * D; }
+inline bool valu_depth_ok(int MX, int R, int D) {
+    for (int d : kValuDepths)
+        if (d == D) return valu_loads(MX, R, D) <= 48;
+    return false;
+}
+// Smallest depth covering a split's blocks in one pass, else the deepest.
+inline int valu_depth(int MX, int R, int blocks) {
+    int best = 0;
+    for (int d : kValuDepths) {
+        if (valu_loads(MX, R, d) > 48) break;
+        best = d;
+        if (d >= blocks) break;
+    }
+    return best;
+}
 
 int stream_xs(int MT, int nst);
 
@@ -112,23 +152,40 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
     const int mt = cdiv(Mc, 16);
+    const int KST = cdiv(K, 512);
     for (const TableEntry& e : kTable) {
         if (e.N == N && e.K == K && e.epilogue == epilogue && Mc >= e.m_lo && Mc <= e.m_hi) {
             *c = e.cfg;
             c->m_tiles = mt;
             if (c->kernel == KRK_KERNEL_MFMA_LDS) c->waves = 4, c->unroll = 1;
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
+            if (c->kernel == KRK_KERNEL_VALU) {
+                c->m_tiles = valu_mx(Mc);
+                c->unroll = valu_depth(c->m_tiles, c->n_tiles, cdiv(KST, c->splits));
+            }
             return;
         }
     }
-    // Other shapes: the persistent stream kernel where x is large and the
-    // weight stream long (its x-in-registers design pays off), otherwise the
-    // LDS-staged MFMA kernel with K split until ~200 workgroups stream.
+    // Other shapes.  M <= 8: the VALU row-streaming kernel, K split until
+    // about 600 workgroup-splits stream and the x slice fits LDS.  Larger M:
+    // the persistent stream kernel where x is large and the weight stream
+    // long (its x-in-registers design pays off), otherwise the LDS-staged
+    // MFMA kernel with K split until ~200 workgroups stream.
     const int Nout = silu ? N / 2 : N;
-    const int KST = cdiv(K, 512);
     krk_gemm_config r{};
     r.m_tiles = mt;
-    if (Mc > 32 && (silu || N >= 65536)) {
+    if (Mc <= kValuMaxRows) {
+        r.kernel = KRK_KERNEL_VALU;
+        r.m_tiles = valu_mx(Mc);
+        r.n_tiles = (silu || Mc > 4) ? 2 : 1;
+        r.waves = 4;
+        const int nblocks = cdiv(Nout, r.waves * (silu ? r.n_tiles / 2 : r.n_tiles));
+        r.splits = 1;
+        while (r.splits < KST && r.splits < 32 &&
+               (nblocks * r.splits < 600 || krk::valu_lds_bytes(r.m_tiles, cdiv(KST, r.splits)) > kLdsBudget))
+            ++r.splits;
+        r.unroll = valu_depth(r.m_tiles, r.n_tiles, cdiv(KST, r.splits));
+    } else if (Mc > 32 && (silu || N >= 65536)) {
         r.kernel = KRK_KERNEL_STREAM;
         r.n_tiles = 1;
         r.waves = 8;
@@ -243,15 +300,30 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
     } else if (c.kernel == KRK_KERNEL_VALU) {
         if (Mc > kValuMaxRows)
             return fail(KRK_ERR_UNSUPPORTED, "VALU kernel handles M <= %d, got %d", kValuMaxRows, M);
-        c.m_tiles = 0;
-        if (!c.n_tiles) c.n_tiles = 1;
-        if (!c.unroll) c.unroll = 1;
-        if (!c.waves) c.waves = 4;
-        if (!c.splits) c.splits = 1;
+        const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
+        c.m_tiles = valu_mx(Mc);
+        if (!c.n_tiles) c.n_tiles = same_kernel ? a.n_tiles : 2;
+        if (!c.waves) c.waves = same_kernel ? a.waves : 8;
+        if (!c.splits) c.splits = same_kernel ? a.splits : 1;
         if (c.n_tiles != 1 && c.n_tiles != 2 && c.n_tiles != 4)
-            return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles=%d not in {1,2,4}", c.n_tiles);
-        if (c.unroll != 1 && c.unroll != 2 && c.unroll != 4)
-            return fail(KRK_ERR_UNSUPPORTED, "VALU unroll=%d not in {1,2,4}", c.unroll);
+            return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles (W rows per wave)=%d not in {1,2,4}", c.n_tiles);
+        if (silu && c.n_tiles % 2)
+            return fail(KRK_ERR_UNSUPPORTED, "SILU_MUL needs an even n_tiles (gate and up rows), got %d", c.n_tiles);
+        if (c.waves != 1 && c.waves != 2 && c.waves != 4 && c.waves != krk::kValuMaxWaves)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU waves=%d not in {1,2,4,%d}", c.waves, krk::kValuMaxWaves);
+        const int nb = cdiv(K, krk::kValuBlock);
+        if (c.splits < 1 || c.splits > 32 || c.splits > nb)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU splits=%d not in 1..min(32, %d K blocks)", c.splits, nb);
+        const int per = cdiv(nb, c.splits);
+        if (!c.unroll) c.unroll = valu_depth(c.m_tiles, c.n_tiles, per);
+        if (!valu_depth_ok(c.m_tiles, c.n_tiles, c.unroll))
+            return fail(KRK_ERR_UNSUPPORTED, "VALU unroll (blocks in flight)=%d not instantiated for %d rows per wave",
+                        c.unroll, c.n_tiles);
+        if (krk::valu_lds_bytes(c.m_tiles, per) > kLdsMax)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU x slice of %zu bytes exceeds LDS (raise splits)",
+                        krk::valu_lds_bytes(c.m_tiles, per));
+        *out = c;
+        return KRK_OK;
     } else {
         return fail(KRK_ERR_UNSUPPORTED, "unknown kernel %d", c.kernel);
     }
@@ -418,9 +490,74 @@ int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, 
     return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
 
+template <int MX, int R, int D, bool SILU>
+int launch_valu(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream) {
+    const int nb = cdiv(a.K, krk::kValuBlock);
+    int per = nb / a.splits, rem = nb % a.splits;
+    // Whole 512-element blocks and whole D-block chunks in every split: the
+    // kernel variant without clamps or masks.
+    const bool exact = a.K % krk::kValuBlock == 0 && rem == 0 && per % D == 0;
+    const void* fn = exact ? reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true>)
+                           : reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false>);
+    const size_t shm = krk::valu_lds_bytes(MX, cdiv(nb, a.splits));
+    if (MX >= krk::kValuLdsMinRows) {
+        static const hipError_t attr[2] = {
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax)};
+        if (attr[exact] != hipSuccess) return hip_status(attr[exact], "valu_gemm_kernel LDS attribute");
+    }
+    void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy, (void*)&a.M,
+                    (void*)&a.N, (void*)&a.K,   (void*)&per, (void*)&rem, (void*)&a.part, (void*)&a.ctr};
+    hipError_t e = hipLaunchKernel(fn, dim3(nblocks, a.splits), dim3(64 * waves), args, shm, stream);
+    return hip_status(e, "valu_gemm_kernel launch");
+}
+
+template <int MX, int R, int D, bool SILU>
+int launch_valu_if(const LaunchArgs& a, int nblocks, int waves, hipStream_t s) {
+    constexpr int loads = (MX < krk::kValuLdsMinRows ? MX + R : R) * D;
+    if constexpr (loads <= 48) {
+        return launch_valu<MX, R, D, SILU>(a, nblocks, waves, s);
+    } else {
+        return fail(KRK_ERR_UNSUPPORTED, "VALU unroll=%d with %d rows per wave", D, R);
+    }
+}
+
+template <int MX, int R, bool SILU>
+int dispatch_valu_d(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    switch (c.unroll) {
+        case 2: return launch_valu_if<MX, R, 2, SILU>(a, nblocks, c.waves, s);
+        case 3: return launch_valu_if<MX, R, 3, SILU>(a, nblocks, c.waves, s);
+        case 4: return launch_valu_if<MX, R, 4, SILU>(a, nblocks, c.waves, s);
+        case 5: return launch_valu_if<MX, R, 5, SILU>(a, nblocks, c.waves, s);
+        case 7: return launch_valu_if<MX, R, 7, SILU>(a, nblocks, c.waves, s);
+        case 8: return launch_valu_if<MX, R, 8, SILU>(a, nblocks, c.waves, s);
+        case 10: return launch_valu_if<MX, R, 10, SILU>(a, nblocks, c.waves, s);
+        case 19: return launch_valu_if<MX, R, 19, SILU>(a, nblocks, c.waves, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "VALU unroll=%d with %d rows per wave", c.unroll, R);
+}
+
+template <int MX, bool SILU>
+int dispatch_valu_r(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    if constexpr (!SILU) {
+        if (c.n_tiles == 1) return dispatch_valu_d<MX, 1, false>(a, c, nblocks, s);
+    }
+    if (c.n_tiles == 2) return dispatch_valu_d<MX, 2, SILU>(a, c, nblocks, s);
+    if (c.n_tiles == 4) return dispatch_valu_d<MX, 4, SILU>(a, c, nblocks, s);
+    return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles=%d", c.n_tiles);
+}
+
 template <bool SILU>
-int dispatch_valu(const LaunchArgs&, const krk_gemm_config&, int, hipStream_t) {
-    return fail(KRK_ERR_UNSUPPORTED, "VALU kernel not built yet");
+int dispatch_valu(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    switch (c.m_tiles) {
+        case 1: return dispatch_valu_r<1, SILU>(a, c, nblocks, s);
+        case 2: return dispatch_valu_r<2, SILU>(a, c, nblocks, s);
+        case 4: return dispatch_valu_r<4, SILU>(a, c, nblocks, s);
+        case 8: return dispatch_valu_r<8, SILU>(a, c, nblocks, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "VALU x rows=%d", c.m_tiles);
 }
 
 int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,

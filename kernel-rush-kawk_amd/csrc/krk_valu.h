@@ -1,0 +1,294 @@
+// VALU row-streaming kernel for the GEMV regime (M <= 8).
+//
+// Each wave owns R rows of W and walks them along K in blocks of 512 elements:
+// one global load per row and block, 64 lanes x 16 contiguous bytes, so every
+// load instruction is a single 1 KB run of one row (the access pattern that
+// reaches the HBM ceiling; the MFMA fragment layout cuts rows into 64-byte
+// pieces and does not).  Lane l always multiplies W[row][k0 + 8l .. 8l+7] by
+// x[m][k0 + 8l .. 8l+7]; products accumulate in fp32 with v_dot2c_f32_bf16
+// (exact bf16 products, fp32 sums).  A wave issues the loads of up to D blocks
+// of all its rows before it consumes the first, so with a few waves per SIMD
+// the whole weight stream of a small projection is in flight at once.
+//
+// x comes from one of two places:
+//   * MX <= 2: straight from global memory (L2-resident after the first
+//     workgroup) into registers, issued just before the W loads of the same
+//     blocks so it arrives first; no LDS, no barrier;
+//   * MX >= 4: once per workgroup into LDS by LDS DMA (global_load_lds),
+//     issued before the W loads, so the workgroup barrier that publishes x
+//     waits only for x, never for W.
+// At the end each wave folds its MX*R per-lane sums across the 64 lanes with
+// a fixed butterfly (gfx950 permlane swaps across rows, DPP within a row), so
+// the summation order — and the result — depends only on the shape.
+//
+// Replaces the reference's Gemv (_gemv_kernel, engine/kernels/gemm.py:248-281,
+// 10-31 and the gate/up variant 35-73) and the M <= 8 SkinnyMatmul configs
+// (gemm.py:364-375); K splits reduce through splitk_finish like the other
+// kernels (gemm.py:96-104, 160-170).
+#pragma once
+
+#include "krk_epilogue.h"
+#include "krk_sync.h"
+
+namespace krk {
+
+constexpr int kValuBlock = 512;  // K elements per wave-wide 16-byte load
+constexpr int kValuMaxWaves = 8;
+constexpr int kValuLdsMinRows = 4;  // x rows from which x is staged in LDS
+
+// Dynamic LDS of one workgroup: x rows [0, MX) of one split's K range, whole
+// 512-element blocks (none when x stays in registers).
+__host__ __device__ constexpr size_t valu_lds_bytes(int MX, int blocks) {
+    return MX < kValuLdsMinRows ? 0 : (size_t)MX * blocks * kValuBlock * sizeof(uint16_t);
+}
+
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
+
+// 16-byte loads at a wave-uniform row base plus a 32-bit byte offset (the
+// scalar-base addressing form of gfx9 global loads: no 64-bit address math
+// per load).
+__device__ __forceinline__ u32x4 load_row16_nt(const uint16_t* base, uint32_t byte_off) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off));
+}
+__device__ __forceinline__ u32x4 load_row16(const uint16_t* base, uint32_t byte_off) {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Partner of a lane in the butterfly step on bit STEP.  Across rows (32, 16)
+// the gfx950 permlane swaps exchange whole rows; within a row DPP row_mirror
+// (lane i <-> 15 - i), row_half_mirror (i <-> 7 - i) and quad_perm (i ^ 2,
+// i ^ 1).  Each partner differs from the lane in bit STEP.
+template <int STEP>
+__device__ __forceinline__ float partner(float v) {
+    if constexpr (STEP == 8) return dpp_move<0x140>(v);
+    if constexpr (STEP == 4) return dpp_move<0x141>(v);
+    if constexpr (STEP == 2) return dpp_move<0x4E>(v);
+    if constexpr (STEP == 1) return dpp_move<0xB1>(v);
+    return v;
+}
+
+// Sum of a lane's pair (lo, hi) with its partner's on the bit-STEP step:
+// lanes with the bit clear get lo + partner's lo, the others hi + partner's hi.
+template <int STEP>
+__device__ __forceinline__ float fold_pair(float lo, float hi, int lane) {
+    if constexpr (STEP == 32 || STEP == 16) {
+        // permlane swap (vdst = lo, src = hi): with the bit clear vdst keeps
+        // the lane's lo and src receives the partner's lo; with it set vdst
+        // receives the partner's hi and src keeps the lane's hi.
+        const auto r = STEP == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false)
+                                  : __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        const bool up = (lane & STEP) != 0;
+        const float give = up ? lo : hi;
+        const float keep = up ? hi : lo;
+        return keep + partner<STEP>(give);
+    }
+}
+
+// Fold N values per lane across the wave.  While N > 1 each step keeps half of
+// the values (the lane's bit STEP picks which half) and adds the partner's
+// copy of that half; once N == 1 each step adds the partner's value.
+// Afterwards lane l holds the wave sum of value (l >> (6 - p)) & (N0 - 1),
+// N0 = 2^p the starting count.
+template <int N, int STEP>
+__device__ __forceinline__ void wave_fold(float* v, int lane) {
+    if constexpr (STEP >= 1) {
+        if constexpr (N > 1) {
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) v[i] = fold_pair<STEP>(v[i], v[i + N / 2], lane);
+            wave_fold<N / 2, STEP / 2>(v, lane);
+        } else {
+            v[0] = fold_pair<STEP>(v[0], v[0], lane);
+            wave_fold<1, STEP / 2>(v, lane);
+        }
+    }
+}
+
+template <int V>
+constexpr int log2_exact() {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "power of two up to 64");
+    if constexpr (V == 1) {
+        return 0;
+    } else {
+        return 1 + log2_exact<V / 2>();
+    }
+}
+
+// MX: x rows held (>= M); R: W rows per wave (for SILU R/2 gate rows then the
+// matching R/2 up rows); D: 512-element blocks loaded per row before the wave
+// consumes them; EXACT: K is whole blocks and every split is whole chunks of D
+// blocks, so no load needs clamping and no lane masking.
+// Grid: x = output blocks, y = K splits; blockDim = 64 x waves; each workgroup
+// covers waves * R (SILU: waves * R/2) consecutive output channels.  Split s
+// owns K blocks [s*per + min(s, rem), ...) where per = nb / splits and
+// rem = nb % splits (nb = ceil(K / 512)), so no division runs on the device.
+template <int MX, int R, int D, bool SILU, bool EXACT>
+__global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w, int64_t ldw,
+    uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int per, int rem,
+    float* __restrict__ part, uint32_t* __restrict__ ctr) {
+    static_assert(!SILU || R % 2 == 0, "SILU pairs gate and up rows");
+    constexpr bool XLDS = MX >= kValuLdsMinRows;
+    static_assert(((XLDS ? 0 : MX) + R) * D < 64, "vmcnt counts at most 63 loads");
+    constexpr int RO = SILU ? R / 2 : R;  // output channels per wave
+    constexpr int V = MX * R;
+    constexpr int P = log2_exact<V>();
+    extern __shared__ __align__(16) unsigned char xs[];
+
+    const int lane = threadIdx.x & 63;
+    // Wave-uniform values live in scalar registers, so every load below is a
+    // scalar row base plus this lane's 32-bit offset.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int waves = blockDim.x >> 6;
+    const int s = blockIdx.y;
+    const int splits = gridDim.y;
+    const int blk = blockIdx.x;
+    const int Nout = SILU ? N / 2 : N;
+    const int cb = waves * RO;
+    const int c0 = blk * cb;
+
+    // This split's K range in whole blocks: [b0, b1), the last possibly ragged.
+    const int nb = (K + kValuBlock - 1) / kValuBlock;
+    const int b0 = s * per + (s < rem ? s : rem);
+    const int b1 = b0 + per + (s < rem ? 1 : 0);
+    const uint32_t lane_k = 8u * (uint32_t)lane;
+
+    // Row bases.  Channels past Nout read the last row (discarded at the end);
+    // x rows past M read row M - 1 (their sums are never stored).
+    const uint16_t* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int c = c0 + wave * RO + (r % RO);
+        c = c < Nout ? c : Nout - 1;
+        const int row = (SILU && r >= RO) ? c + Nout : c;
+        wrow[r] = w + (int64_t)row * ldw;
+    }
+    const uint16_t* xrow[MX];
+#pragma unroll
+    for (int m = 0; m < MX; ++m) xrow[m] = x + (int64_t)(m < M ? m : M - 1) * ldx;
+
+    // Element offset of this lane's 8 elements of block bb.  Generic shapes
+    // clamp bb into the split (surplus loads of a short last chunk repeat a
+    // block and are not consumed) and send lanes past K to k = 0 (zeroed).
+    auto koff = [&](int bb) -> uint32_t {
+        if constexpr (EXACT) {
+            return (uint32_t)bb * kValuBlock + lane_k;
+        } else {
+            bb = bb < b1 ? bb : b1 - 1;
+            const uint32_t k = (uint32_t)bb * kValuBlock + lane_k;
+            return k < (uint32_t)K ? k : 0u;
+        }
+    };
+
+    u32x4 wv[D][R];
+    u32x4 xv[XLDS ? 1 : D][MX];
+    auto issue = [&](int b) {
+        if constexpr (!XLDS) {
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int m = 0; m < MX; ++m) xv[d][m] = load_row16(xrow[m], 2u * koff(b + d));
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+            for (int r = 0; r < R; ++r) wv[d][r] = load_row16_nt(wrow[r], 2u * koff(b + d));
+    };
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+    const bool ragged = (K % kValuBlock) != 0;
+    // Consume the chunk of D blocks at b: each block as soon as its loads land.
+    auto consume = [&](int b) {
+        const int n = b1 - b;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (EXACT || d < n) {
+                const int bb = b + d;
+                // Keep each block's LDS reads of x with that block.
+                if constexpr (XLDS) __builtin_amdgcn_sched_barrier(0);
+                u32x4 xb[MX];
+#pragma unroll
+                for (int m = 0; m < MX; ++m) {
+                    if constexpr (XLDS) {
+                        xb[m] = *reinterpret_cast<const u32x4*>(
+                            xs + ((size_t)(m * (b1 - b0) + (bb - b0)) * kValuBlock + lane_k) * 2);
+                    } else {
+                        xb[m] = xv[d][m];
+                    }
+                }
+                if (!EXACT && ragged && bb == nb - 1 && (uint32_t)bb * kValuBlock + lane_k >= (uint32_t)K) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) wv[d][r] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+                    for (int m = 0; m < MX; ++m) xb[m] = u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (int m = 0; m < MX; ++m) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float a = acc[m * R + r];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(wv[d][r][j]), as_bf16x2(xb[m][j]), a, false);
+                        acc[m * R + r] = a;
+                    }
+                }
+            }
+        }
+    };
+
+    // Each chunk's loads are issued and consumed in the same iteration (no
+    // registers carried across iterations); the whole K range of a split is
+    // usually one chunk.
+    int b = b0;
+    if constexpr (XLDS) {
+        // x[0:MX, b0*512 : b1*512) into LDS as [m][block][512], one 1 KB DMA
+        // per (row, block), spread over the waves; the first W loads go out
+        // behind them.  The barrier publishes x after a full vmcnt drain: the
+        // compiler may move plain W loads across the barrier, so a partial
+        // count could let a DMA still be in flight.
+        const int nblk = b1 - b0;
+        int m = 0, bi = wave;
+        while (bi >= nblk) bi -= nblk, ++m;
+        for (int j = wave; j < MX * nblk; j += waves) {
+            dma_row(xrow[m] + koff(b0 + bi), xs + (size_t)j * (kValuBlock * 2));
+            bi += waves;
+            while (bi >= nblk) bi -= nblk, ++m;
+        }
+        issue(b0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        vm_wait<0>();
+        bare_barrier();
+        consume(b0);
+        b += D;
+    }
+    for (; b < b1; b += D) {
+        issue(b);
+        consume(b);
+    }
+
+    wave_fold<V, 32>(acc, lane);
+
+    // Lane l now holds value v = (l >> (6 - P)) & (V - 1), i.e. (m, r) with
+    // v = m * R + r; the first lane of each group of 2^(6-P) writes it.
+    constexpr int G = 64 >> P;  // lanes per value
+    const int v = (lane >> (6 - P)) & (V - 1);
+    const int m = v / R;
+    const int r = v - m * R;
+    float u = 0.0f;
+    if constexpr (SILU) u = __shfl_down(acc[0], RO * G);
+    const OutStage<SILU> o{y, ldy, part, M, N, Nout, splits, s};
+    const int c = c0 + wave * RO + r;
+    if ((lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
+    if (splits > 1) splitk_finish<SILU>(o, ctr, blk, c0, cb);
+}
+
+}  // namespace krk

@@ -71,8 +71,8 @@ def test_argument_errors(lib, kw, code, msg):
 
 
 def _split_shape(lib):
-    """A shape whose plan splits K (down_proj at M = 1) and its workspace size."""
-    M, N, K = 1, 2560, 9728
+    """A shape whose plan splits K (down_proj at M = 4) and its workspace size."""
+    M, N, K = 4, 2560, 9728
     cfg = GemmConfig()
     assert lib.krk_gemm_plan(M, N, K, NONE, ctypes.byref(cfg)) == 0 and cfg.splits > 1
     need = lib.krk_gemm_workspace_bytes(M, N, K, NONE)
@@ -83,6 +83,8 @@ def _split_shape(lib):
 def _channels_per_block(c, epi):
     if c["kernel"] == _lib.KERNEL_STREAM:
         return 8 if epi == SILU else 16
+    if c["kernel"] == _lib.KERNEL_VALU:
+        return c["waves"] * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
     return 16 * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
 
 
@@ -131,8 +133,11 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
     cfg = GemmConfig()
     assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
     c = cfg.as_dict()
-    assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM)
-    assert 16 * c["m_tiles"] >= min(M, 64) and c["m_tiles"] <= 4
+    assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM, _lib.KERNEL_VALU)
+    if c["kernel"] == _lib.KERNEL_VALU:
+        assert M <= 8 and c["m_tiles"] in (1, 2, 4, 8) and c["m_tiles"] >= M
+    else:
+        assert 16 * c["m_tiles"] >= min(M, 64) and c["m_tiles"] <= 4
     assert c["splits"] >= 1 and c["waves"] >= 1
     if c["kernel"] != _lib.KERNEL_STREAM:
         nout = N // 2 if epi == SILU else N
@@ -154,6 +159,32 @@ def test_config_errors(lib, cfg, code, msg):
     rc = lib.krk_gemm_bf16_config(X, 2560, W, 2560, Y, 6144, 20, 6144, 2560, NONE, ctypes.byref(c), 0, 0, None)
     assert rc == code
     assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("cfg,msg", [
+    (dict(kernel=2, n_tiles=3), "n_tiles"),
+    (dict(kernel=2, unroll=6), "unroll"),
+    (dict(kernel=2, n_tiles=4, unroll=19), "unroll"),
+    (dict(kernel=2, waves=16), "waves"),
+    (dict(kernel=2, splits=6), "splits"),
+])
+def test_valu_config_errors(lib, cfg, msg):
+    """K = 2560 is five 512-element blocks: at most 5 splits."""
+    c = GemmConfig.from_dict(cfg)
+    rc = lib.krk_gemm_bf16_config(X, 2560, W, 2560, Y, 6144, 4, 6144, 2560, NONE, ctypes.byref(c), 0, 0, None)
+    assert rc == _lib.KRK_ERR_UNSUPPORTED
+    assert msg in _lib.last_error()
+
+
+def test_valu_x_slice_must_fit_lds(lib):
+    """M = 8 keeps 8 x rows of a split's K range in LDS: K = 16384 unsplit is
+    256 KB, over gfx950's 160 KB, and is refused; two splits fit."""
+    c = GemmConfig.from_dict(dict(kernel=2, splits=1))
+    assert lib.krk_gemm_config_workspace_bytes(8, 512, 16384, NONE, ctypes.byref(c)) == 0
+    rc = lib.krk_gemm_bf16_config(X, 16384, W, 16384, Y, 512, 8, 512, 16384, NONE, ctypes.byref(c), 0, 0, None)
+    assert rc == _lib.KRK_ERR_UNSUPPORTED and "LDS" in _lib.last_error()
+    c = GemmConfig.from_dict(dict(kernel=2, splits=2))
+    assert lib.krk_gemm_config_workspace_bytes(8, 512, 16384, NONE, ctypes.byref(c)) > 0
 
 
 def test_silu_needs_even_tiles(lib):

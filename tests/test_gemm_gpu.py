@@ -306,6 +306,13 @@ def _stream_configs(M, K):
         yield dict(kernel=_lib.KERNEL_STREAM, m_tiles=mt, splits=sp, unroll=d)
 
 
+def _valu_configs(silu, depths=(2, 3, 5, 7, 19)):
+    for wv, nt, d, sp in itertools.product((1, 8), (1, 2, 4), depths, (1, 3)):
+        if silu and nt % 2:
+            continue
+        yield dict(kernel=_lib.KERNEL_VALU, waves=wv, n_tiles=nt, unroll=d, splits=sp)
+
+
 def _run_configs(x, w, epi, configs):
     """Run every configuration the library accepts; check each against the oracle."""
     ref = R.gateup_bf16(x, w) if epi == SILU else R.linear_bf16(x, w)
@@ -347,6 +354,40 @@ def test_gateup_configs_all_kernels(device, M, I, K):
     x = R.randn_bf16((M, K), 8900 + M)
     w = R.randn_bf16((2 * I, K), 8901 + I, 0.02)
     _run_configs(x, w, SILU, itertools.chain(_lds_configs(M, True), _stream_configs(M, K)))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 96, 1536), (3, 200, 1000), (8, 130, 2568), (5, 4099, 520), (2, 40, 8),
+                                   (7, 33, 4096)])
+def test_all_valu_configs_agree(device, M, N, K):
+    """Row-streaming VALU kernel: every (waves, rows per wave, blocks in flight,
+    splits) choice, with a ragged last K block (lanes past K masked), K below
+    one block, and channel counts that leave a workgroup partly empty."""
+    x = R.randn_bf16((M, K), 9100 + M)
+    w = R.randn_bf16((N, K), 9101 + N, 0.02)
+    _run_configs(x, w, NONE, _valu_configs(False))
+
+
+@pytest.mark.parametrize("M,I,K", [(1, 40, 1536), (8, 52, 1000), (4, 9, 2568)])
+def test_valu_gateup_configs(device, M, I, K):
+    x = R.randn_bf16((M, K), 9200 + M)
+    w = R.randn_bf16((2 * I, K), 9201 + I, 0.02)
+    _run_configs(x, w, SILU, _valu_configs(True))
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_valu_qwen_shapes(device, M):
+    """The VALU kernel on the real projection shapes, including down's 19
+    K blocks (several passes of the block loop) and the widest split."""
+    for name, (N, K, epi) in {"qkv": (6144, 2560, NONE), "o": (2560, 4096, NONE), "down": (2560, 9728, NONE),
+                              "gate_up": (19456, 2560, SILU)}.items():
+        x = R.randn_bf16((M, K), 9300 + M + K)
+        w = R.randn_bf16((N, K), 9301 + N, 0.02)
+        cfgs = [dict(kernel=_lib.KERNEL_VALU, n_tiles=2, waves=8, unroll=5, splits=1),
+                dict(kernel=_lib.KERNEL_VALU, n_tiles=4, waves=4, unroll=4, splits=2)]
+        if name == "down":
+            cfgs.append(dict(kernel=_lib.KERNEL_VALU, n_tiles=1, waves=8, unroll=10, splits=1))
+            cfgs.append(dict(kernel=_lib.KERNEL_VALU, n_tiles=2, waves=8, unroll=3, splits=4))
+        _run_configs(x, w, epi, cfgs)
 
 
 @pytest.mark.parametrize("M", [1, 8, 33, 64])
