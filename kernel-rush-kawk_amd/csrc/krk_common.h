@@ -20,9 +20,10 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
 // fp32 -> bf16 bits, round to nearest even.  NaN stays NaN (quiet bit set),
 // infinities and overflow to infinity follow IEEE rounding.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (u >> 16) | 0x40u;
+    return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;  // a select, not a branch
 }
 
 __device__ __forceinline__ float round_bf16(float f) {

@@ -108,8 +108,8 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 25, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 16, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
     {2560, 9728, KRK_EPILOGUE_NONE, 2, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 3)},
@@ -119,8 +119,10 @@ const TableEntry kTable[] = {
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 4, 0, 0, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 4, 0, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 33, 48, kcfg(KRK_KERNEL_STREAM, 1, 3, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
 };
 
 // VALU: x rows held per launch (a power of two >= M), and the instantiated
@@ -217,9 +219,10 @@ int stream_xs(int MT, int nst) {
         if (xs && xs >= nst) return xs;
     return 0;
 }
+// Deepest ring that leaves room for one output-buffer block.
 inline int stream_max_depth(int MT) {
     int d = krk::kStreamMaxDepth;
-    while (d > 2 && krk::stream_lds_bytes(MT, d) > kLdsMax) --d;
+    while (d > 2 && krk::stream_lds_bytes(MT, d) + krk::stream_out_bytes(MT, false) > kLdsMax) --d;
     return d;
 }
 // Persistent grid: workgroups per split, at most one per CU, chosen so the
@@ -442,13 +445,24 @@ int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks
 template <int MT, int XS, bool SILU>
 int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream) {
     const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU>);
-    const size_t shm = krk::stream_lds_bytes(MT, depth);
-    if (shm > kLdsMax) return fail(KRK_ERR_UNSUPPORTED, "STREAM needs %zu bytes of LDS", shm);
+    size_t shm = krk::stream_lds_bytes(MT, depth);
+    const int G = stream_groups(nblocks, a.splits);
+    // Unsplit K: the rest of the LDS holds finished blocks until the end.
+    int obcap = 0;
+    if (a.splits == 1) {
+        const size_t per = krk::stream_out_bytes(MT, SILU);
+        const size_t room = shm < kLdsMax ? (kLdsMax - shm) / per : 0;
+        const int blocks_per_wg = cdiv(nblocks, G);
+        obcap = (int)(room < (size_t)blocks_per_wg ? room : (size_t)blocks_per_wg);
+        shm += (size_t)obcap * per;
+    }
+    if (shm > kLdsMax || (a.splits == 1 && obcap < 1))
+        return fail(KRK_ERR_UNSUPPORTED, "STREAM depth %d leaves no LDS for the output buffer", depth);
     static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
     if (attr != hipSuccess) return hip_status(attr, "stream_gemm_kernel LDS attribute");
-    const int groups = stream_groups(nblocks, a.splits) * a.splits;
+    const int groups = G * a.splits;
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
-                    (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth,
+                    (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth, (void*)&obcap,
                     (void*)&a.part, (void*)&a.ctr};
     hipError_t e = hipLaunchKernel(fn, dim3(groups), dim3(64 * krk::kStreamWaves), args, shm, stream);
     return hip_status(e, "stream_gemm_kernel launch");

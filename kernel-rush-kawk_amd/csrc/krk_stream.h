@@ -44,11 +44,15 @@ constexpr int kStreamKPW = (kStreamKC / 32) / kStreamWaves;  // k-steps per wave
 constexpr int kStreamLPW = 16 / kStreamWaves;                // DMAs per wave per stage (2)
 constexpr int kStreamMaxDepth = 8;
 
-// Bytes of dynamic LDS: reduction area [WV][MT][64] f32x4, then the ring.
+// Bytes of dynamic LDS: two reduction areas [WV][MT][64] f32x4 (blocks
+// alternate between them), then the ring.
 __host__ __device__ constexpr size_t stream_red_bytes(int MT) { return (size_t)kStreamWaves * MT * 64 * 16; }
 __host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth) {
-    return stream_red_bytes(MT) + (size_t)depth * kStreamSlot;
+    return 2 * stream_red_bytes(MT) + (size_t)depth * kStreamSlot;
 }
+// Output buffer behind the ring (unsplit K): the bf16 results of `obcap`
+// blocks, [slot][16·MT rows][CB channels].
+__host__ __device__ constexpr size_t stream_out_bytes(int MT, bool silu) { return (size_t)(silu ? 8 : 16) * 16 * MT * 2; }
 
 // MT: 16-row m tiles (M <= 16·MT).  XS: most K stages a workgroup owns (its
 // x fragments live in X[XS][2][MT]).  SILU: gate/up blocks with the epilogue.
@@ -57,7 +61,7 @@ __global__ void __launch_bounds__(512)
 stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                    const uint16_t* __restrict__ w, int64_t ldw,
                    uint16_t* __restrict__ y, int64_t ldy,
-                   int M, int N, int K, int splits, int depth,
+                   int M, int N, int K, int splits, int depth, int obcap,
                    float* __restrict__ part, uint32_t* __restrict__ ctr) {
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     constexpr int WV = kStreamWaves;
@@ -66,8 +70,11 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     constexpr int CB = SILU ? 8 : 16;  // output channels per block
 
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    f32x4* const red = reinterpret_cast<f32x4*>(smem);
-    unsigned char* const ring = smem + stream_red_bytes(MT);
+    f32x4* const red0 = reinterpret_cast<f32x4*>(smem);
+    f32x4* const red1 = red0 + WV * MT * 64;
+    unsigned char* const ring = smem + 2 * stream_red_bytes(MT);
+    uint16_t* const ob = reinterpret_cast<uint16_t*>(ring + (size_t)depth * kStreamSlot);
+    constexpr int MP = 16 * MT;  // rows per output-buffer slot
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -141,6 +148,82 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
 
     OutStage<SILU> o{y, ldy, part, M, N, Nout, splits, s};
+    // Global stores share vmcnt with the ring's DMAs on gfx9, so a store in
+    // the stage loop makes the following ring waits stricter and stalls the
+    // storing waves.  With K unsplit the block results therefore go to an
+    // LDS output buffer, written to y with 16-byte stores only when the
+    // buffer is full (rare) and at the end.  Split K keeps the fp32 partials
+    // and the fix-up of splitk_finish.
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && ((ldy & 7) == 0);
+    auto flush = [&](int base, int cnt) {  // local blocks base .. base+cnt-1 in slots 0 .. cnt-1
+        constexpr int CPR = CB / 8;         // 16-byte chunks per row
+        const int items = cnt * M * CPR;
+        for (int it = threadIdx.x; it < items; it += blockDim.x) {
+            const int ch = it % CPR;
+            const int rest = it / CPR;
+            const int m = rest % M;
+            const int sl = rest / M;
+            const int c0 = (gi + (base + sl) * Gs) * CB + 8 * ch;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(ob + ((size_t)(sl * MP + m) * CB + 8 * ch));
+            uint16_t* dst = y + (int64_t)m * ldy + c0;
+            if (vec_ok && c0 + 8 <= Nout) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (c0 + e < Nout) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+    };
+    // Block epilogue: each thread finishes output elements (m, c) of the
+    // block, summing the eight waves' partials in fixed wave order (8 or 16
+    // independent LDS reads, then the adds).  It runs inside the next
+    // block's first stage, after that stage's barrier (which also publishes
+    // the partials) and its DMA issue, so the ring keeps streaming while it
+    // works.  Partial layout: rb[wave][m tile][lane] f32x4, lane (r, q) holds
+    // rows 4q..4q+3 of channel r.
+    auto finish_block = [&](int bl, const f32x4* rb) {
+        const int b = gi + bl * Gs;
+        const int sl = obcap > 0 ? bl % obcap : 0;
+        if (splits == 1 && sl == 0 && bl > 0) {
+            // Buffer full: write it out before slot 0 is reused.
+            flush(bl - obcap, obcap);
+            lds_wait();
+            bare_barrier();
+        }
+        const float* rf = reinterpret_cast<const float*>(rb);
+        constexpr int LS = SILU ? 8 : 16;    // channels of a 16-row tile with outputs
+        constexpr int LSB = SILU ? 3 : 4;    // log2(LS)
+        constexpr int ITEMS = MT * 4 * LS * 4;
+        for (int it = threadIdx.x; it < ITEMS; it += blockDim.x) {
+            const int e = it & 3;
+            const int rr = (it >> 2) & (LS - 1);
+            const int qq = (it >> (2 + LSB)) & 3;
+            const int i = it >> (4 + LSB);
+            const int ln = rr + 16 * qq;
+            const int m = 16 * i + 4 * qq + e;
+            float gv[WV], uv[WV];
+#pragma unroll
+            for (int wv = 0; wv < WV; ++wv) {
+                gv[wv] = rf[((wv * MT + i) * 64 + ln) * 4 + e];
+                if (SILU) uv[wv] = rf[((wv * MT + i) * 64 + (ln ^ 8)) * 4 + e];
+            }
+            float g = gv[0], u = SILU ? uv[0] : 0.0f;
+#pragma unroll
+            for (int wv = 1; wv < WV; ++wv) {
+                g += gv[wv];
+                if (SILU) u += uv[wv];
+            }
+            const int c = b * CB + rr;
+            if (splits == 1) {
+                ob[(size_t)(sl * MP + m) * CB + rr] = (uint16_t)(SILU ? silu_mul_bf16(g, u) : f32_to_bf16(g));
+            } else if (m < M && c < Nout) {
+                o.put(m, c, g, u);
+            }
+        }
+        if (splits > 1) splitk_finish<SILU>(o, ctr, b, b * CB, CB);
+    };
+
     int t = 0;
     for (int bi = 0; bi < myblocks; ++bi) {
         const int b = gi + bi * Gs;
@@ -154,6 +237,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 vm_wait_stages<LPW>(min(depth - 2, T - 1 - t));
                 bare_barrier();  // stage t landed for every wave; the slot of t-1 is free
                 if (t + depth - 1 < T) issue(t + depth - 1);
+                if (j == 0 && bi > 0) finish_block(bi - 1, (bi & 1) ? red0 : red1);
                 const unsigned char* slot = ring + (size_t)(t % depth) * kStreamSlot;
                 const bool ktail = (sb + j + 1) * kStreamKC > K;
 #pragma unroll
@@ -171,36 +255,23 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             }
         }
 
-        // Block epilogue: every wave parks its partial sums, one barrier, then
-        // thread v sums lane-slot v over the waves in fixed order.  The area
-        // is rewritten only after the next block's stage barriers.
+        // Park this block's partial sums; the next stage barrier publishes
+        // them.  Buffer bi % 2 was last read by the epilogue of block bi - 2,
+        // which ran before at least one barrier this wave has since passed.
+        f32x4* const rb = (bi & 1) ? red1 : red0;
 #pragma unroll
-        for (int i = 0; i < MT; ++i) red[(wave * MT + i) * 64 + lane] = acc[i];
+        for (int i = 0; i < MT; ++i) rb[(wave * MT + i) * 64 + lane] = acc[i];
         lds_wait();
+    }
+    if (myblocks > 0) {
         bare_barrier();
-        const int v = threadIdx.x;
-        if (v < MT * 64) {
-            const int i = v >> 6;
-            const int ln = v & 63;
-            const int rr = ln & 15;
-            const int mb = 16 * i + 4 * (ln >> 4);
-            if (!SILU || rr < 8) {
-                f32x4 g = red[(0 * MT + i) * 64 + ln];
-                f32x4 u = SILU ? red[(0 * MT + i) * 64 + (ln ^ 8)] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int wv = 1; wv < WV; ++wv) {
-                    g += red[(wv * MT + i) * 64 + ln];
-                    if (SILU) u += red[(wv * MT + i) * 64 + (ln ^ 8)];
-                }
-                const int c = b * CB + rr;
-                if (c < Nout) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (mb + e < M) o.put(mb + e, c, g[e], u[e]);
-                }
-            }
+        finish_block(myblocks - 1, ((myblocks - 1) & 1) ? red1 : red0);
+        if (splits == 1) {
+            lds_wait();
+            bare_barrier();
+            const int base = (myblocks - 1) / obcap * obcap;
+            flush(base, myblocks - base);
         }
-        if (splits > 1) splitk_finish<SILU>(o, ctr, b, b * CB, CB);
     }
 }
 
