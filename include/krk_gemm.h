@@ -110,7 +110,7 @@ typedef struct krk_gemm_config {
     int unroll;   /* k-steps loaded per pipeline stage (MFMA: 2, 4, 8; VALU: 1, 2, 4;
                      MFMA_LDS: ignored, a stage is 512 k); STREAM: ring depth in
                      512-k stages (2..8) */
-    int waves;    /* waves per workgroup (1, 2, 4; MFMA_LDS: 4; STREAM: 8, n_tiles 1) */
+    int waves;    /* waves per workgroup (MFMA: 1, 2, 4; VALU: 1, 2, 4, 8; MFMA_LDS and STREAM: 8) */
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
 } krk_gemm_config;
 

@@ -100,9 +100,8 @@ const TableEntry kTable[] = {
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 9, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 25, 32, kcfg(KRK_KERNEL_MFMA_LDS, 1, 0, 0, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 2)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 0, 0, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 17, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
@@ -159,7 +158,7 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
         if (e.N == N && e.K == K && e.epilogue == epilogue && Mc >= e.m_lo && Mc <= e.m_hi) {
             *c = e.cfg;
             c->m_tiles = mt;
-            if (c->kernel == KRK_KERNEL_MFMA_LDS) c->waves = 4, c->unroll = 1;
+            if (c->kernel == KRK_KERNEL_MFMA_LDS) c->waves = krk::kLdsWaves, c->unroll = 1;
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
             if (c->kernel == KRK_KERNEL_VALU) {
                 c->m_tiles = valu_mx(Mc);
@@ -198,7 +197,7 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
         r.kernel = KRK_KERNEL_MFMA_LDS;
         r.n_tiles = (N >= 65536 && Mc > 8) ? 4 : 2;
         r.unroll = 1;
-        r.waves = 4;
+        r.waves = krk::kLdsWaves;
         const int nblocks = cdiv(Nout, 16 * (silu ? r.n_tiles / 2 : r.n_tiles));
         r.splits = 1;
         while (nblocks * r.splits < 192 && r.splits < 4 && KST >= 2 * (r.splits + 1)) ++r.splits;
@@ -282,6 +281,10 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
             return fail(KRK_ERR_UNSUPPORTED, "SILU_MUL needs an even n_tiles, got %d", c.n_tiles);
         if (c.waves != krk::kLdsWaves)
             return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS runs %d waves per workgroup, got waves=%d", krk::kLdsWaves, c.waves);
+        if (c.splits < 1 || c.splits > 32)
+            return fail(KRK_ERR_UNSUPPORTED, "splits=%d not in 1..32", c.splits);
+        *out = c;
+        return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_STREAM) {
         if (!c.m_tiles) c.m_tiles = cdiv(Mc, 16);
         c.n_tiles = 1;
