@@ -103,6 +103,9 @@ def main() -> int:
     ap.add_argument("--no-torch", action="store_true", help="skip the torch-GPU comparison timings")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample length")
+    ap.add_argument("--profile-dominant", action="store_true",
+                    help="only replay the dominant kernel (gate_up at --M over 36 layer weights, 3 graph replays) "
+                         "and a 256 MiB device copy: the workload the committed rocprofv3 --pmc summaries measure")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -122,6 +125,9 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
+
+    if args.profile_dominant:
+        return profile_dominant(torch, G, dev, args.M)
 
     # ------------------------------------------------------------ weights
     t0 = time.time()
@@ -199,8 +205,9 @@ def main() -> int:
     dom_ms, _ = graph_time_ms(torch, dom_calls, reps=max(5, args.steps // 4))
     dom_bytes = algo_bytes(dom, M)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic = measured_traffic(dom, M, ops[dom].resolved_config)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                 "kernel": f"{dom} M={M} ({KERNEL_NAMES[ops[dom].resolved_config['kernel']]}, SiLU*mul)",
                 "config": ops[dom].resolved_config, "us_per_launch": round(dom_ms * 1000, 2),
                 "bytes_per_launch": dom_bytes}
@@ -264,6 +271,46 @@ def main() -> int:
         "per_gemm": table,
     }
     print(json.dumps(result), flush=True)
+    return 0
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "stream_gemm_gate_up_M32_traffic.json"
+
+
+def measured_traffic(name: str, M: int, config: dict):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, each scaled by what
+    the counter reads for a device copy of known size), when that summary was
+    taken on this exact kernel configuration; None otherwise."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if rec.get("shape") != name or rec.get("M") != M or rec.get("config") != config:
+        return None
+    return rec.get("traffic_bytes_per_launch")
+
+
+def profile_dominant(torch, G, dev, M: int) -> int:
+    """Workload for the counter runs: 3 replays of a graph of 36 gate_up
+    launches (distinct layer weights, as in the sweep), then 4 copies of a
+    256 MiB buffer for the counters' byte calibration."""
+    K, Nw, _ = SHAPES["gate_up"]
+    ws = [randn_bf16(torch, (Nw, K), seed_for(4, l, "gate_up"), 0.02, dev) for l in range(LAYERS)]
+    x = randn_bf16(torch, (M, K), seed_for(4, 0, "x") + K, 1.0, dev)
+    op = G.SkinnyGateUp(M, Nw // 2, K, dev)
+    out = torch.empty((M, Nw // 2), dtype=torch.bfloat16, device=dev)
+    calls = [(lambda w=w: op.run(x, w, out)) for w in ws]
+    _, g = graph_time_ms(torch, calls, reps=1)
+    for _ in range(3):
+        g.replay()
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "dominant", "shape": "gate_up", "M": M, "config": op.resolved_config,
+                      "copy_bytes": 256 << 20, "copies": 4}), flush=True)
     return 0
 
 
