@@ -99,7 +99,7 @@ enum {
     KRK_KERNEL_MFMA = 1,   /* bf16 MFMA 16x16x32 tiles, W fragments straight from HBM */
     KRK_KERNEL_VALU = 2,   /* dot2 row streaming in 512-k blocks (M <= 8); x in registers
                               (M <= 2) or staged once in LDS (M > 2) */
-    KRK_KERNEL_MFMA_LDS = 3, /* bf16 MFMA 16x16x32, W streamed row-contiguously through LDS */
+    KRK_KERNEL_MFMA_LDS = 3, /* bf16 MFMA 16x16x32, W and x rows streamed row-contiguously through LDS */
     KRK_KERNEL_STREAM = 5   /* persistent bf16 MFMA: W through an LDS DMA ring, x held in registers */
 };
 
@@ -111,10 +111,13 @@ typedef struct krk_gemm_config {
                      SILU_MUL); VALU: W rows per wave (1, 2, 4; even with SILU_MUL) */
     int unroll;   /* MFMA: k-steps loaded per pipeline stage (2, 4, 8); VALU: 512-k
                      blocks in flight per row (2, 3, 4, 5, 7, 8, 10, 19, at most 48
-                     loads in flight per lane); MFMA_LDS: ignored, a stage is 512 k;
-                     STREAM: ring depth in 512-k stages (2..8, less at large M) */
+                     loads in flight per lane); MFMA_LDS: stages in flight (2, or 3
+                     when m_tiles + n_tiles <= 6); STREAM: ring depth in 512-k
+                     stages (2..8, less at large M) */
     int waves;    /* waves per workgroup (MFMA: 1, 2, 4; VALU: 1, 2, 4, 8; MFMA_LDS and STREAM: 8) */
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
+    int k_chunk;  /* MFMA_LDS: k per pipeline stage, 256 or 512 (512 needs
+                     m_tiles + n_tiles <= 4); other kernels: ignored */
 } krk_gemm_config;
 
 /*

@@ -68,7 +68,15 @@ struct OutStage {
 
 // Called by every thread of the workgroup after all put() calls.  `blk` is the
 // block's counter index, [c0, c0 + cb) its output channels.
-template <bool SILU>
+//
+// The partials live beyond this XCD's L2, so each load is a full round trip
+// (about a microsecond).  The last workgroup therefore issues the loads of
+// kBatch splits for kElems elements before it adds anything, and adds them in
+// split order afterwards: one round trip per batch instead of one per split.
+// The loaded values occupy 2·kBatch·kElems VGPRs, so kernels that call this
+// with their main-loop registers still live (the persistent stream kernel)
+// use kBatch = kElems = 1.
+template <bool SILU, int kBatch = 8, int kElems = 2>
 __device__ void splitk_finish(const OutStage<SILU>& o, uint32_t* __restrict__ ctr,
                               int blk, int c0, int cb) {
     __shared__ int is_last;
@@ -81,19 +89,53 @@ __device__ void splitk_finish(const OutStage<SILU>& o, uint32_t* __restrict__ ct
     __syncthreads();
     if (!is_last) return;
     const int n = cb < o.Nout - c0 ? cb : o.Nout - c0;
+    const int total = o.M * n;
     const int64_t sstride = (int64_t)o.M * o.N;
-    for (int e = threadIdx.x; e < o.M * n; e += blockDim.x) {
-        const int m = e / n;
-        const int c = c0 + (e - m * n);
-        const float* p = o.part + (int64_t)m * o.N + c;
-        float g = load_agent(p);
-        float u = SILU ? load_agent(p + o.Nout) : 0.0f;
-        for (int s = 1; s < o.splits; ++s) {
-            g += load_agent(p + s * sstride);
-            if (SILU) u += load_agent(p + s * sstride + o.Nout);
+    for (int e0 = threadIdx.x; e0 < total; e0 += kElems * blockDim.x) {
+        const float* p[kElems];
+        float g[kElems], u[kElems];
+#pragma unroll
+        for (int h = 0; h < kElems; ++h) {
+            int e = e0 + h * blockDim.x;
+            e = e < total ? e : e0;  // a spare slot re-reads element e0 and is not stored
+            const int m = e / n;
+            p[h] = o.part + (int64_t)m * o.N + c0 + (e - m * n);
+            g[h] = 0.0f;
+            u[h] = 0.0f;
         }
-        const uint32_t v = SILU ? silu_mul_bf16(g, u) : f32_to_bf16(g);
-        o.y[(int64_t)m * o.ldy + c] = (uint16_t)v;
+        for (int s0 = 0; s0 < o.splits; s0 += kBatch) {
+            float gv[kElems][kBatch], uv[kElems][kBatch];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                if (s0 + b < o.splits) {
+#pragma unroll
+                    for (int h = 0; h < kElems; ++h) {
+                        gv[h][b] = load_agent(p[h] + (s0 + b) * sstride);
+                        if (SILU) uv[h][b] = load_agent(p[h] + (s0 + b) * sstride + o.Nout);
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                if (s0 + b < o.splits) {
+#pragma unroll
+                    for (int h = 0; h < kElems; ++h) {
+                        // Split 0 starts the sum (0 + v would turn -0 into +0).
+                        g[h] = (s0 + b == 0) ? gv[h][b] : g[h] + gv[h][b];
+                        if (SILU) u[h] = (s0 + b == 0) ? uv[h][b] : u[h] + uv[h][b];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < kElems; ++h) {
+            const int e = e0 + h * blockDim.x;
+            if (e < total) {
+                const int m = e / n;
+                const uint32_t v = SILU ? silu_mul_bf16(g[h], u[h]) : f32_to_bf16(g[h]);
+                o.y[(int64_t)m * o.ldy + c0 + (e - m * n)] = (uint16_t)v;
+            }
+        }
     }
     if (threadIdx.x == 0) {
         __hip_atomic_store(ctr + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

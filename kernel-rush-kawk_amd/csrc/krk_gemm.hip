@@ -84,24 +84,24 @@ struct TableEntry {
     int N, K, epilogue, m_lo, m_hi;
     krk_gemm_config cfg;  // m_tiles 0: derived from M
 };
-constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits) {
-    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits};
+constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits, int k_chunk = 0) {
+    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk};
 }
 // VALU entries: n_tiles = W rows per wave, unroll 0 = blocks in flight chosen
-// to cover a split's K range in one pass.
+// to cover a split's K range in one pass.  MFMA_LDS entries: unroll = stages in
+// flight, k_chunk 0 = 512 where it fits.
 const TableEntry kTable[] = {
     // qkv 2560 -> 6144
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
     {6144, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 3, 8, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 9, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 5, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1)},
     // o_proj 4096 -> 2560
     {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 0, 0, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 17, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 17, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
@@ -111,14 +111,12 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 2, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 3)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 9, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 2, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // lm_head 2560 -> 151936
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_MFMA_LDS, 2, 0, 0, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 4, 0, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256)},
     {151936, 2560, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 33, 48, kcfg(KRK_KERNEL_STREAM, 1, 3, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
@@ -149,6 +147,9 @@ inline int valu_depth(int MX, int R, int blocks) {
 
 int stream_xs(int MT, int nst);
 
+// MFMA_LDS k per stage when the caller or the table does not choose one.
+inline int default_kc(int MT, int NT) { return krk::mfma_lds_kc_ok(MT, NT, 512) ? 512 : 256; }
+
 void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     const bool silu = epilogue == KRK_EPILOGUE_SILU_MUL;
@@ -158,7 +159,11 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
         if (e.N == N && e.K == K && e.epilogue == epilogue && Mc >= e.m_lo && Mc <= e.m_hi) {
             *c = e.cfg;
             c->m_tiles = mt;
-            if (c->kernel == KRK_KERNEL_MFMA_LDS) c->waves = krk::kLdsWaves, c->unroll = 1;
+            if (c->kernel == KRK_KERNEL_MFMA_LDS) {
+                c->waves = krk::kLdsWaves;
+                c->unroll = c->unroll ? c->unroll : 2;
+                c->k_chunk = c->k_chunk ? c->k_chunk : default_kc(mt, c->n_tiles);
+            }
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
             if (c->kernel == KRK_KERNEL_VALU) {
                 c->m_tiles = valu_mx(Mc);
@@ -196,7 +201,8 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
     } else {
         r.kernel = KRK_KERNEL_MFMA_LDS;
         r.n_tiles = (N >= 65536 && Mc > 8) ? 4 : 2;
-        r.unroll = 1;
+        r.unroll = 2;
+        r.k_chunk = default_kc(mt, r.n_tiles);
         r.waves = krk::kLdsWaves;
         const int nblocks = cdiv(Nout, 16 * (silu ? r.n_tiles / 2 : r.n_tiles));
         r.splits = 1;
@@ -204,6 +210,11 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
     }
     *c = r;
 }
+
+// MFMA_LDS keeps `unroll` stages of row pieces in registers; three stages fit
+// 256 VGPRs without spilling up to this many 16-row tiles (m + n).
+constexpr int kLdsPf3MaxTiles = 6;
+constexpr bool mfma_lds_pf3(int MT, int NT) { return MT + NT <= kLdsPf3MaxTiles; }
 
 // Dynamic LDS a gfx950 workgroup may use: 160 KB less room for the kernels'
 // static __shared__ variables.
@@ -270,8 +281,10 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
     } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {
         if (!c.m_tiles) c.m_tiles = cdiv(Mc, 16);
         if (!c.n_tiles) c.n_tiles = same_kernel ? a.n_tiles : (epilogue == KRK_EPILOGUE_SILU_MUL ? 2 : 1);
-        if (!c.unroll) c.unroll = 1;
+        if (!c.unroll) c.unroll = same_kernel ? a.unroll : 2;
         if (!c.waves) c.waves = krk::kLdsWaves;
+        if (!c.k_chunk) c.k_chunk = same_kernel && a.m_tiles == c.m_tiles && a.n_tiles == c.n_tiles ? a.k_chunk
+                                                                                                  : default_kc(c.m_tiles, c.n_tiles);
         if (!c.splits) c.splits = same_kernel ? a.splits : 1;
         if (c.m_tiles < cdiv(Mc, 16) || c.m_tiles > 4)
             return fail(KRK_ERR_INVALID, "m_tiles=%d cannot cover %d rows (need %d..4)", c.m_tiles, Mc, cdiv(Mc, 16));
@@ -281,6 +294,12 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
             return fail(KRK_ERR_UNSUPPORTED, "SILU_MUL needs an even n_tiles, got %d", c.n_tiles);
         if (c.waves != krk::kLdsWaves)
             return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS runs %d waves per workgroup, got waves=%d", krk::kLdsWaves, c.waves);
+        if (!krk::mfma_lds_kc_ok(c.m_tiles, c.n_tiles, c.k_chunk))
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS k_chunk=%d: 256, or 512 when m_tiles + n_tiles <= 4 (%d + %d)",
+                        c.k_chunk, c.m_tiles, c.n_tiles);
+        if (c.unroll != 2 && !(c.unroll == 3 && mfma_lds_pf3(c.m_tiles, c.n_tiles)))
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS stages in flight (unroll)=%d not instantiated for %d x %d tiles "
+                        "(2, or 3 when m_tiles + n_tiles <= %d)", c.unroll, c.m_tiles, c.n_tiles, kLdsPf3MaxTiles);
         if (c.splits < 1 || c.splits > 32)
             return fail(KRK_ERR_UNSUPPORTED, "splits=%d not in 1..32", c.splits);
         *out = c;
@@ -409,28 +428,44 @@ int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int NT, bool SILU>
+template <int MT, int NT, int PF, int KC, bool SILU>
 int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, SILU>);
-    const size_t shm = krk::mfma_lds_bytes(MT, NT);
-    // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once per
-    // instantiation (a function attribute, not a stream operation).
-    static const hipError_t attr = shm > 65536 ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm)
-                                               : hipSuccess;
-    if (attr != hipSuccess) return hip_status(attr, "mfma_lds_kernel LDS attribute");
-    void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
-                    (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr};
-    hipError_t e = hipLaunchKernel(fn, dim3(nblocks * a.splits), dim3(64 * krk::kLdsWaves), args, shm, stream);
-    return hip_status(e, "mfma_lds_kernel launch");
+    if constexpr ((PF == 3 && !mfma_lds_pf3(MT, NT)) || !krk::mfma_lds_kc_ok(MT, NT, KC)) {
+        return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS unroll=%d k_chunk=%d with %d x %d tiles", PF, KC, MT, NT);
+    } else {
+        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU>);
+        const size_t shm = krk::mfma_lds_bytes(MT, NT, KC);
+        // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once
+        // per instantiation (a function attribute, not a stream operation).
+        static const hipError_t attr =
+            shm > 65536 ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) : hipSuccess;
+        if (attr != hipSuccess) return hip_status(attr, "mfma_lds_kernel LDS attribute");
+        void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
+                        (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr};
+        hipError_t e = hipLaunchKernel(fn, dim3(nblocks * a.splits), dim3(64 * krk::kLdsWaves), args, shm, stream);
+        return hip_status(e, "mfma_lds_kernel launch");
+    }
+}
+
+template <int MT, int NT, int KC, bool SILU>
+int dispatch_mfma_lds_pf(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, KC, SILU>(a, nblocks, s);
+    return launch_mfma_lds<MT, NT, 2, KC, SILU>(a, nblocks, s);
+}
+
+template <int MT, int NT, bool SILU>
+int dispatch_mfma_lds_kc(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    if (c.k_chunk == 512) return dispatch_mfma_lds_pf<MT, NT, 512, SILU>(a, c, nblocks, s);
+    return dispatch_mfma_lds_pf<MT, NT, 256, SILU>(a, c, nblocks, s);
 }
 
 template <int MT, bool SILU>
 int dispatch_mfma_lds_n(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
     if constexpr (!SILU) {
-        if (c.n_tiles == 1) return launch_mfma_lds<MT, 1, false>(a, nblocks, s);
+        if (c.n_tiles == 1) return dispatch_mfma_lds_kc<MT, 1, false>(a, c, nblocks, s);
     }
-    if (c.n_tiles == 2) return launch_mfma_lds<MT, 2, SILU>(a, nblocks, s);
-    if (c.n_tiles == 4) return launch_mfma_lds<MT, 4, SILU>(a, nblocks, s);
+    if (c.n_tiles == 2) return dispatch_mfma_lds_kc<MT, 2, SILU>(a, c, nblocks, s);
+    if (c.n_tiles == 4) return dispatch_mfma_lds_kc<MT, 4, SILU>(a, c, nblocks, s);
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS n_tiles=%d", c.n_tiles);
 }
 

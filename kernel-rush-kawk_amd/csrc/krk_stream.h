@@ -221,7 +221,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 o.put(m, c, g, u);
             }
         }
-        if (splits > 1) splitk_finish<SILU>(o, ctr, b, b * CB, CB);
+        if (splits > 1) splitk_finish<SILU, 1, 1>(o, ctr, b, b * CB, CB);
     };
 
     int t = 0;

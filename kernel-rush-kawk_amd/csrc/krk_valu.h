@@ -288,7 +288,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     const OutStage<SILU> o{y, ldy, part, M, N, Nout, splits, s};
     const int c = c0 + wave * RO + r;
     if ((lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
-    if (splits > 1) splitk_finish<SILU>(o, ctr, blk, c0, cb);
+    if (splits > 1) splitk_finish<SILU, 4, 1>(o, ctr, blk, c0, cb);
 }
 
 }  // namespace krk

@@ -41,7 +41,7 @@ _size = ctypes.c_size_t
 
 
 class GemmConfig(ctypes.Structure):
-    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits."""
+    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk."""
 
     _fields_ = [
         ("kernel", _int),
@@ -50,6 +50,7 @@ class GemmConfig(ctypes.Structure):
         ("unroll", _int),
         ("waves", _int),
         ("splits", _int),
+        ("k_chunk", _int),
     ]
 
     def as_dict(self) -> dict:

@@ -153,6 +153,11 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
     (dict(kernel=1, waves=8), _lib.KRK_ERR_UNSUPPORTED, "waves"),
     (dict(kernel=1, splits=33), _lib.KRK_ERR_UNSUPPORTED, "splits"),
     (dict(kernel=2), _lib.KRK_ERR_UNSUPPORTED, "VALU"),
+    (dict(kernel=3, unroll=4), _lib.KRK_ERR_UNSUPPORTED, "unroll"),
+    (dict(kernel=3, m_tiles=4, n_tiles=4, unroll=3), _lib.KRK_ERR_UNSUPPORTED, "unroll"),
+    (dict(kernel=3, waves=4), _lib.KRK_ERR_UNSUPPORTED, "waves"),
+    (dict(kernel=3, m_tiles=2, n_tiles=4, k_chunk=512), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
+    (dict(kernel=3, k_chunk=384), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
 ])
 def test_config_errors(lib, cfg, code, msg):
     c = GemmConfig.from_dict(cfg)

@@ -294,10 +294,10 @@ def test_all_mfma_gateup_configs_agree(device):
 
 def _lds_configs(M, silu):
     mt_min = -(-min(M, 64) // 16)
-    for mt, nt, sp in itertools.product(range(mt_min, 5), (1, 2, 4), (1, 2, 3)):
+    for mt, nt, pf, kc, sp in itertools.product(range(mt_min, 5), (1, 2, 4), (2, 3), (256, 512), (1, 2, 3, 9)):
         if silu and nt % 2:
             continue
-        yield dict(kernel=_lib.KERNEL_MFMA_LDS, m_tiles=mt, n_tiles=nt, splits=sp)
+        yield dict(kernel=_lib.KERNEL_MFMA_LDS, m_tiles=mt, n_tiles=nt, unroll=pf, k_chunk=kc, splits=sp)
 
 
 def _stream_configs(M, K):
@@ -340,6 +340,24 @@ def test_all_lds_configs_agree(device, M, N, K):
     x = R.randn_bf16((M, K), 8700 + M)
     w = R.randn_bf16((N, K), 8701 + N, 0.02)
     _run_configs(x, w, NONE, _lds_configs(M, False))
+
+
+@pytest.mark.parametrize("kernel", [_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_VALU])
+@pytest.mark.parametrize("splits", [8, 9, 16, 17, 32])
+def test_many_splits_fixed_order(device, kernel, splits):
+    """Split counts around and past the fix-up's load batch (8 splits per round
+    trip): the combined result is still a correct fp32 rounding, and equal
+    for repeated calls."""
+    M, N, K = (5, 96, 32768) if kernel == _lib.KERNEL_VALU else (20, 96, 32768)
+    x = R.randn_bf16((M, K), 9100 + splits)
+    w = R.randn_bf16((N, K), 9101, 0.02)
+    cfg = dict(kernel=kernel, splits=splits)
+    say("many splits", kernel, splits, M, N, K)
+    y = krk(x, w, NONE, cfg)
+    assert_parity(y, R.linear_bf16(x, w), f"config {cfg}")
+    exact, mag = R.linear_exact(x, w)
+    assert R.within_fp32_bound(y, exact, mag, K).all(), f"config {cfg}"
+    assert torch.equal(y, krk(x, w, NONE, cfg))
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 96, 1536), (13, 200, 1000), (40, 96, 2568), (64, 130, 520), (5, 4099, 2048)])
