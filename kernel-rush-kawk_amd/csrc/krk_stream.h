@@ -20,7 +20,8 @@
 //     the fragments of its fixed share of k-steps (2 of every stage's 16) for
 //     every stage of the workgroup's K range — so x costs one L2 read per CU
 //     instead of one per block, and no load in the loop competes with the
-//     ring in the in-order vmcnt counter.
+//     ring in the in-order vmcnt counter.  It is read as whole 1 KB row
+//     pieces and turned into fragments through LDS before the ring starts.
 //   * Waits are explicit (vmcnt = DMAs issued after the consumed stage) and
 //     barriers carry no memory fence, so the compiler never drains the ring.
 //
@@ -118,33 +119,55 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             dma_row(w + (int64_t)wr * ldw + kc, slot + row * kStreamPitch);
         }
     };
-    for (int d = 0; d < depth - 1 && d < T; ++d) issue(d);
-
-    // x fragments of this wave's k-steps, rows past M and k past K zeroed.
+    // x for the workgroup's K range, loaded once.  Whole 1 KB row pieces (wave
+    // w loads rows w, w + 8, ... of every stage): a CU pulls L2 data ~2.5x
+    // faster this way than in the MFMA fragment pattern.  Rows past M, k past
+    // K and stages past the split's range are zero.
+    constexpr int LX = 2 * MT;  // 16·MT rows over 8 waves
+    u32x4 XR[XS][LX];
+#pragma unroll
+    for (int j = 0; j < XS; ++j) {
+        const int k = (sb + j) * kStreamKC + klane;
+        const bool kok = j < nst && k < K;
+#pragma unroll
+        for (int i = 0; i < LX; ++i) {
+            const int m = wave + WV * i;
+            const u32x4 v = load_cached16(x + (int64_t)(m < M ? m : M - 1) * ldx + (kok ? k : 0));
+            XR[j][i] = (kok && m < M) ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    // Each stage's rows go through LDS (the reduction areas, 16·MT rows of
+    // 1 KB, idle until the first block ends; chunks XOR-swizzled by row so the
+    // fragment reads hit distinct banks) and come back as this wave's MFMA
+    // fragments: X[j][kk][i], lane (r, q) = x[16i + r][32·(KPW·wave + kk) + 8q
+    // .. +7] of stage j.
     u32x4 X[XS][KPW][MT];
+    unsigned char* const xstage = smem;
 #pragma unroll
     for (int j = 0; j < XS; ++j) {
 #pragma unroll
-        for (int kk = 0; kk < KPW; ++kk) {
-            const int k = (sb + j) * kStreamKC + 32 * (wave * KPW + kk) + 8 * q;
-            const bool kok = j < nst && k < K;
-#pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const int m = 16 * i + r;
-                const bool ok = kok && m < M;
-                u32x4 v = load_cached16(x + (int64_t)(m < M ? m : M - 1) * ldx + (kok ? k : 0));
-                v &= ok ? 0xffffffffu : 0u;
-                X[j][kk][i] = v;
-            }
+        for (int i = 0; i < LX; ++i) {
+            const int m = wave + WV * i;
+            *reinterpret_cast<u32x4*>(xstage + m * 1024 + 16 * (lane ^ (m & 15))) = XR[j][i];
         }
+        lds_wait();
+        bare_barrier();
+#pragma unroll
+        for (int kk = 0; kk < KPW; ++kk) {
+            const int c = 4 * (wave * KPW + kk) + q;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+                X[j][kk][i] = *reinterpret_cast<const u32x4*>(xstage + (16 * i + r) * 1024 + 16 * (c ^ r));
+        }
+        lds_wait();
+        bare_barrier();
     }
-
-    // Everything issued so far — the ring prologue, then x — must land before
-    // the first stage: x is read-only from here on and the compiler then
-    // knows it is complete (it would otherwise wait for it behind the ring on
-    // every use).  The x transfer overlaps the prologue's HBM latency.
-    vm_wait<0>();
+    // The weight ring starts only now.  Measured: with its prologue in flight
+    // the first-touch HBM fills of x queue behind 256 workgroups' worth of
+    // weight DMAs and the x preload takes ~1.7x longer than the ring latency
+    // it would hide.
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    for (int d = 0; d < depth - 1 && d < T; ++d) issue(d);
 
 
     OutStage<SILU> o{y, ldy, part, M, N, Nout, splits, s};
