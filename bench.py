@@ -242,6 +242,49 @@ def main() -> int:
                 log(f"M={Mt:3d} {name:8s} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s {row['pct_peak']:5.1f}%"
                     + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
 
+    # ------------------------------------------------------------ normed projections
+    # The qkv, gate_up and lm_head calls of a decode step take rms_norm(x + y)
+    # as input (the reference's pick_normed contract).  Three ways of running
+    # one, each over the same rotating weights: the library's normed call
+    # (one launch where the plan fuses the prologue), the stand-alone prologue
+    # kernel followed by the plain projection (two launches), and the torch
+    # composition followed by F.linear.
+    normed = []
+    if not args.no_table:
+        eps = 1e-6
+        for Mt in (1, 4, 8, 32, 64):
+            for name in ("qkv", "gate_up", "lm_head"):
+                K, Nw, silu = SHAPES[name]
+                xt = randn_bf16(torch, (Mt, K), 91 + Mt, 1.0, dev)
+                yt = randn_bf16(torch, (Mt, K), 92 + Mt, 0.5, dev)
+                wn = randn_bf16(torch, (K,), 93, 1.0, dev)
+                xo = torch.empty_like(xt)
+                op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
+                ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
+                ws = lm if name == "lm_head" else [L[name] for L in layers]
+                n = 2 * len(ws) if name == "lm_head" else len(ws)
+                fused_ms, _ = graph_time_ms(torch, [(lambda w=ws[i % len(ws)]: op.run(xt, w, ot, norm=(yt, wn, xo, eps)))
+                                                    for i in range(n)])
+                two_ms, _ = graph_time_ms(torch, [(lambda w=ws[i % len(ws)]: op.run(G.add_rms_norm(xt, yt, wn, eps, xout=xo), w, ot))
+                                                  for i in range(n)])
+                row = {"shape": name, "M": Mt, "us": round(fused_ms * 1000, 2),
+                       "prologue_kernel_plus_gemm_us": round(two_ms * 1000, 2),
+                       "one_launch": G.normed_fused(Mt, Nw, K, G.EPILOGUE_SILU_MUL if silu else G.EPILOGUE_NONE)}
+                if not args.no_torch:
+                    def torch_normed(w):
+                        s_ = (xt.float() + yt.float()).to(torch.bfloat16)
+                        sf = s_.float()
+                        nrm = ((sf * torch.rsqrt((sf * sf).mean(-1, keepdim=True) + eps)).to(torch.bfloat16).float()
+                               * wn.float()).to(torch.bfloat16)
+                        r = F.linear(nrm, w)
+                        return F.silu(r[:, :INTER]) * r[:, INTER:] if silu else r
+                    tms, _ = graph_time_ms(torch, [(lambda w=ws[i % len(ws)]: torch_normed(w)) for i in range(n)])
+                    row["torch_gpu_us"] = round(tms * 1000, 2)
+                normed.append(row)
+                log(f"normed M={Mt:3d} {name:8s} {row['us']:8.2f} us ({'1 launch' if row['one_launch'] else '2 launches'})"
+                    f"   prologue+gemm {row['prologue_kernel_plus_gemm_us']:8.2f} us"
+                    + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
+
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -269,6 +312,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "per_gemm": table,
+        "normed": normed,
     }
     print(json.dumps(result), flush=True)
     return 0

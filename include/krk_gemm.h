@@ -151,6 +151,69 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx,
                          void* stream);
 
 /*
+ * krk_gemm_bf16_normed — a projection with the residual-add + RMSNorm
+ * prologue fused in front:
+ *
+ *   xout = bf16(x + d)
+ *   n    = bf16(bf16(xout · rsqrt(mean(xout²) + eps)) · w_norm)   (mean in fp32)
+ *   y    = epilogue(n · Wᵀ)
+ *
+ * Replaces the reference's normed call f(x, y, w_norm, xout, w) that
+ * pick_normed returns (engine/kernels/gemm.py:501-560), i.e.
+ * SkinnyMatmul.__call__(a, w, norm=(y, w_norm, xout, eps)) (gemm.py:346-361)
+ * and SkinnyGateUp.__call__(a, wg, wu, norm=...) (gemm.py:314-329); the
+ * rounding points are those of gemm.py:21-51 and add_rmsnorm.py:15-29.  `d`
+ * is the reference's `y` (the branch output added to the residual x).
+ *
+ *   x, d       [M, K] bf16, strides ldx, ldd (multiples of 8, 16-byte aligned)
+ *   w_norm     [K] bf16 RMSNorm gain; eps >= 0
+ *   xout       [M, K] bf16 output, stride ldxo; may not overlap x, d, w_norm, W, y
+ *   w, y, M, N, K, epilogue, stream   as krk_gemm_bf16 (K <= 16384)
+ *   workspace  krk_gemm_normed_workspace_bytes(M, N, K, epilogue, NULL) bytes;
+ *              its split-K counters must be zero before first use (every call
+ *              leaves them zero); the rest is scratch.
+ *
+ * At M = 1, VALU plans of at most 2048 workgroups run the prologue inside the
+ * projection kernel (one launch); krk_gemm_normed_fused tells which.  Other
+ * calls run a one-workgroup-per-row prologue kernel that writes xout and the
+ * normalised rows into the workspace, then the projection.
+ */
+int krk_gemm_bf16_normed(const void* x, int64_t ldx, const void* d, int64_t ldd,
+                         const void* w_norm, float eps, void* xout, int64_t ldxo,
+                         const void* w, int64_t ldw, void* y, int64_t ldy,
+                         int M, int N, int K, int epilogue,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* krk_gemm_bf16_normed with an explicit configuration (as krk_gemm_bf16_config). */
+int krk_gemm_bf16_normed_config(const void* x, int64_t ldx, const void* d, int64_t ldd,
+                                const void* w_norm, float eps, void* xout, int64_t ldxo,
+                                const void* w, int64_t ldw, void* y, int64_t ldy,
+                                int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of krk_gemm_bf16_normed(_config); cfg may be NULL (the
+ * plan).  0 for an invalid shape or configuration. */
+size_t krk_gemm_normed_workspace_bytes(int M, int N, int K, int epilogue, const krk_gemm_config* cfg);
+
+/* 1 when the normed call for this shape and configuration (NULL = the plan)
+ * runs the prologue inside the projection kernel, 0 when it launches the
+ * separate prologue kernel first, negative on an invalid shape/config. */
+int krk_gemm_normed_fused(int M, int N, int K, int epilogue, const krk_gemm_config* cfg);
+
+/*
+ * krk_add_rms_norm_bf16 — the stand-alone prologue: xout = bf16(x + d) and
+ * out = bf16(bf16(xout · rstd) · w_norm) per row, one workgroup per row.
+ * Replaces add_rms_norm (engine/kernels/add_rmsnorm.py:32-43), which the
+ * reference's unfused path launches in front of a plain projection
+ * (engine/model.py:161-171).  K <= 16384; xout may be x itself (same pointer
+ * and stride: in place, as the reference allows); otherwise xout and out may
+ * not overlap each other or the inputs.
+ */
+int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd,
+                          const void* w_norm, float eps, void* xout, int64_t ldxo,
+                          void* out, int64_t ldo, int M, int K, void* stream);
+
+/*
  * krk_last_error — text of the last error raised on the calling thread by
  * any krk_* function ("" if none).  Stands in for the ValueError messages of
  * engine/kernels/gateup64.py:63-74 and engine/kernels/gemm.py:253-254.

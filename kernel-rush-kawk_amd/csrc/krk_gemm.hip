@@ -12,9 +12,12 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <utility>
+
 #include "krk_gemm.h"
 #include "krk_mfma.h"
 #include "krk_mfma_lds.h"
+#include "krk_norm.h"
 #include "krk_stream.h"
 #include "krk_valu.h"
 
@@ -542,26 +545,26 @@ int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, 
     return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
 
-template <int MX, int R, int D, bool SILU>
-int launch_valu(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream) {
+template <int MX, int R, int D, bool SILU, bool NORM = false>
+int launch_valu(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream, krk::NormArgs na = {}) {
     const int nb = cdiv(a.K, krk::kValuBlock);
     int per = nb / a.splits, rem = nb % a.splits;
     // Whole 512-element blocks and whole D-block chunks in every split: the
     // kernel variant without clamps or masks.
     const bool exact = a.K % krk::kValuBlock == 0 && rem == 0 && per % D == 0;
-    const void* fn = exact ? reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true>)
-                           : reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false>);
-    const size_t shm = krk::valu_lds_bytes(MX, cdiv(nb, a.splits));
-    if (MX >= krk::kValuLdsMinRows) {
+    const void* fn = exact ? reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM>)
+                           : reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM>);
+    const size_t shm = NORM ? krk::valu_norm_lds_bytes(MX, nb) : krk::valu_lds_bytes(MX, cdiv(nb, a.splits));
+    if (NORM || MX >= krk::kValuLdsMinRows) {
         static const hipError_t attr[2] = {
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax),
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax)};
         if (attr[exact] != hipSuccess) return hip_status(attr[exact], "valu_gemm_kernel LDS attribute");
     }
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy, (void*)&a.M,
-                    (void*)&a.N, (void*)&a.K,   (void*)&per, (void*)&rem, (void*)&a.part, (void*)&a.ctr};
+                    (void*)&a.N, (void*)&a.K,   (void*)&per, (void*)&rem, (void*)&a.part, (void*)&a.ctr, (void*)&na};
     hipError_t e = hipLaunchKernel(fn, dim3(nblocks, a.splits), dim3(64 * waves), args, shm, stream);
     return hip_status(e, "valu_gemm_kernel launch");
 }
@@ -612,9 +615,75 @@ int dispatch_valu(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "VALU x rows=%d", c.m_tiles);
 }
 
+// The fused RMSNorm prologue is instantiated for the VALU depth that covers a
+// K of 2560 (the hidden size every normed projection reads) in one pass.
+constexpr int kValuNormDepth = 5;
+
+template <int MX, bool SILU>
+int dispatch_valu_norm_r(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                         const krk::NormArgs& na) {
+    if constexpr (!SILU) {
+        if (c.n_tiles == 1) return launch_valu<MX, 1, kValuNormDepth, false, true>(a, nblocks, c.waves, s, na);
+    }
+    if (c.n_tiles == 2) return launch_valu<MX, 2, kValuNormDepth, SILU, true>(a, nblocks, c.waves, s, na);
+    if (c.n_tiles == 4) return launch_valu<MX, 4, kValuNormDepth, SILU, true>(a, nblocks, c.waves, s, na);
+    return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles=%d", c.n_tiles);
+}
+
+template <bool SILU>
+int dispatch_valu_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                       const krk::NormArgs& na) {
+    if (c.m_tiles == 1) return dispatch_valu_norm_r<1, SILU>(a, c, nblocks, s, na);
+    return fail(KRK_ERR_UNSUPPORTED, "the fused prologue runs at M = 1, got %d x rows", c.m_tiles);
+}
+
+// The fused prologue makes every workgroup stage x and d for the whole K and
+// take the row statistics itself.  Measured on MI355X, that pays only when it
+// is small next to the workgroup's share of W: at M = 1 with at most
+// kNormFusedMaxGroups workgroups (qkv 8.9 vs 9.7 us, gate_up 19.0 vs 19.7 us
+// against the prologue kernel + projection).  lm_head's 19k workgroups lose
+// 15 us at M = 1, and at M = 4..8 the staging rivals the weight stream
+// (gate_up M = 8: 115 vs 23 us), so those run the separate prologue kernel.
+constexpr int kNormFusedMaxGroups = 2048;
+
+// Whether a resolved configuration runs the RMSNorm prologue inside the VALU
+// kernel (else a separate prologue kernel writes the normalised rows first).
+bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
+    if (c.kernel != KRK_KERNEL_VALU || M != 1 || c.unroll != kValuNormDepth) return false;
+    const Geometry g = geometry(M, N, epilogue, c);
+    return (int64_t)g.nblocks * c.splits <= kNormFusedMaxGroups &&
+           krk::valu_norm_lds_bytes(c.m_tiles, cdiv(K, krk::kValuBlock)) <= kLdsMax;
+}
+
+// The residual-add + RMSNorm prologue of a normed call (krk_norm.h).
+struct NormSpec {
+    const void* d;
+    int64_t ldd;
+    const void* w_norm;
+    float eps;
+    void* xout;
+    int64_t ldxo;
+};
+
+// Workspace of a call: [split-K counters and partials][normalised rows
+// M x K bf16 when a separate prologue writes them].
+struct WorkspaceLayout {
+    size_t gemm;    // split-K part, at offset 0
+    size_t n_off;   // offset of the normalised rows (0 if none)
+    size_t total;
+};
+WorkspaceLayout workspace_layout(int M, int N, int K, int epilogue, const krk_gemm_config& c, bool normed) {
+    WorkspaceLayout l;
+    l.gemm = workspace_for(M, N, epilogue, c);
+    const bool prologue = normed && !norm_fused(M, N, K, epilogue, c);
+    l.n_off = prologue ? align_up(l.gemm, 256) : 0;
+    l.total = prologue ? l.n_off + (size_t)M * K * sizeof(uint16_t) : l.gemm;
+    return l;
+}
+
 int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
               int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
-              void* workspace, size_t workspace_bytes, void* stream) {
+              void* workspace, size_t workspace_bytes, void* stream, const NormSpec* ns = nullptr) {
     g_err[0] = '\0';
     int rc = check_shape(M, N, K, epilogue);
     if (rc) return rc;
@@ -626,6 +695,21 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     if ((ldx % 8) || (ldw % 8)) return fail(KRK_ERR_ALIGN, "ldx=%lld and ldw=%lld must be multiples of 8 elements", (long long)ldx, (long long)ldw);
     if (((uintptr_t)x % 16) || ((uintptr_t)w % 16)) return fail(KRK_ERR_ALIGN, "x=%p and w=%p must be 16-byte aligned", x, w);
     if ((uintptr_t)y % 2) return fail(KRK_ERR_ALIGN, "y=%p must be 2-byte aligned", y);
+    if (ns) {
+        if (!ns->d || !ns->w_norm || !ns->xout)
+            return fail(KRK_ERR_INVALID, "null norm operand (d=%p w_norm=%p xout=%p)", ns->d, ns->w_norm, ns->xout);
+        if (ns->ldd < K || ns->ldxo < K)
+            return fail(KRK_ERR_INVALID, "ldd=%lld / ldxo=%lld must be >= K=%d", (long long)ns->ldd, (long long)ns->ldxo, K);
+        if ((ns->ldd % 8) || (ns->ldxo % 8))
+            return fail(KRK_ERR_ALIGN, "ldd=%lld and ldxo=%lld must be multiples of 8 elements", (long long)ns->ldd, (long long)ns->ldxo);
+        if (((uintptr_t)ns->d % 16) || ((uintptr_t)ns->w_norm % 16) || ((uintptr_t)ns->xout % 16))
+            return fail(KRK_ERR_ALIGN, "d, w_norm and xout must be 16-byte aligned");
+        if (!(ns->eps >= 0.0f) || ns->eps == __builtin_inff())
+            return fail(KRK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)ns->eps);
+        if (K > krk::kNormThreads * 8 * krk::kNormMaxVec)
+            return fail(KRK_ERR_UNSUPPORTED, "the RMSNorm prologue handles K <= %d, got %d",
+                        krk::kNormThreads * 8 * krk::kNormMaxVec, K);
+    }
 
     krk_gemm_config c;
     rc = resolve_config(M, N, K, epilogue, cfg, &c);
@@ -636,27 +720,61 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     const uintptr_t y0 = (uintptr_t)y, y1 = y0 + ((uint64_t)(M - 1) * ldy + Nout) * 2;
     if (overlaps(y0, y1, x0, x1) || overlaps(y0, y1, w0, w1))
         return fail(KRK_ERR_ALIAS, "output y may not share memory with x or W");
+    uintptr_t o0 = 0, o1 = 0;
+    if (ns) {
+        // Every workgroup reads all of x and d while one of them writes xout,
+        // so xout may share memory with none of the operands.
+        o0 = (uintptr_t)ns->xout;
+        o1 = o0 + ((uint64_t)(M - 1) * ns->ldxo + K) * 2;
+        const uintptr_t d0 = (uintptr_t)ns->d, d1 = d0 + ((uint64_t)(M - 1) * ns->ldd + K) * 2;
+        const uintptr_t g0 = (uintptr_t)ns->w_norm, g1 = g0 + (uint64_t)K * 2;
+        if (overlaps(o0, o1, x0, x1) || overlaps(o0, o1, d0, d1) || overlaps(o0, o1, g0, g1) ||
+            overlaps(o0, o1, w0, w1) || overlaps(o0, o1, y0, y1))
+            return fail(KRK_ERR_ALIAS, "xout may not share memory with x, d, w_norm, W or y");
+        if (overlaps(y0, y1, d0, d1) || overlaps(y0, y1, g0, g1))
+            return fail(KRK_ERR_ALIAS, "output y may not share memory with d or w_norm");
+    }
 
-    const size_t need = workspace_for(M, N, epilogue, c);
-    if (need) {
-        if (!workspace) return fail(KRK_ERR_WORKSPACE, "this plan needs a %zu-byte workspace, got none", need);
-        if (workspace_bytes < need) return fail(KRK_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, need);
+    const WorkspaceLayout wl = workspace_layout(M, N, K, epilogue, c, ns != nullptr);
+    if (wl.total) {
+        if (!workspace) return fail(KRK_ERR_WORKSPACE, "this plan needs a %zu-byte workspace, got none", wl.total);
+        if (workspace_bytes < wl.total)
+            return fail(KRK_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, wl.total);
         if ((uintptr_t)workspace % 16) return fail(KRK_ERR_ALIGN, "workspace=%p must be 16-byte aligned", workspace);
-        const uintptr_t s0 = (uintptr_t)workspace, s1 = s0 + need;
-        if (overlaps(s0, s1, x0, x1) || overlaps(s0, s1, w0, w1) || overlaps(s0, s1, y0, y1))
-            return fail(KRK_ERR_ALIAS, "workspace may not share memory with x, W or y");
+        const uintptr_t s0 = (uintptr_t)workspace, s1 = s0 + wl.total;
+        if (overlaps(s0, s1, x0, x1) || overlaps(s0, s1, w0, w1) || overlaps(s0, s1, y0, y1) ||
+            (ns && overlaps(s0, s1, o0, o1)))
+            return fail(KRK_ERR_ALIAS, "workspace may not share memory with x, W, y or xout");
     }
 
     const Geometry g = geometry(M, N, epilogue, c);
-    uint32_t* ctr = need ? static_cast<uint32_t*>(workspace) : nullptr;
-    float* part = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                  align_up((size_t)g.nblocks * sizeof(uint32_t), 256))
-                       : nullptr;
+    uint32_t* ctr = wl.gemm ? static_cast<uint32_t*>(workspace) : nullptr;
+    float* part = wl.gemm ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                     align_up((size_t)g.nblocks * sizeof(uint32_t), 256))
+                          : nullptr;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    krk::NormArgs na{};
+    if (ns) na = krk::NormArgs{static_cast<const uint16_t*>(ns->d), ns->ldd, static_cast<const uint16_t*>(ns->w_norm),
+                               ns->eps, static_cast<uint16_t*>(ns->xout), ns->ldxo};
+    const bool fused = ns && norm_fused(M, N, K, epilogue, c);
+    // Projection input: x itself, or the normalised rows a prologue kernel
+    // writes into the workspace.
+    const uint16_t* xin = static_cast<const uint16_t*>(x);
+    int64_t ldin = ldx;
+    if (ns && !fused) {
+        uint16_t* nrows = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + wl.n_off);
+        int64_t ldn = K;
+        void* args[] = {(void*)&x, (void*)&ldx, (void*)&na, (void*)&nrows, (void*)&ldn, (void*)&K};
+        hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&krk::add_rmsnorm_kernel), dim3(M),
+                                       dim3(krk::kNormThreads), args, 0, st);
+        if ((rc = hip_status(e, "add_rmsnorm_kernel launch"))) return rc;
+        xin = nrows;
+        ldin = ldn;
+    }
     for (int m0 = 0; m0 < M; m0 += kMaxRowsPerLaunch) {
         LaunchArgs a;
-        a.x = static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx;
-        a.ldx = ldx;
+        a.x = xin + (int64_t)m0 * ldin;
+        a.ldx = ldin;
         a.w = static_cast<const uint16_t*>(w);
         a.ldw = ldw;
         a.y = static_cast<uint16_t*>(y) + (int64_t)m0 * ldy;
@@ -667,7 +785,9 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
         a.splits = c.splits;
         a.part = part;
         a.ctr = ctr;
-        if (c.kernel == KRK_KERNEL_MFMA) {
+        if (fused) {
+            rc = silu ? dispatch_valu_norm<true>(a, c, g.nblocks, st, na) : dispatch_valu_norm<false>(a, c, g.nblocks, st, na);
+        } else if (c.kernel == KRK_KERNEL_MFMA) {
             rc = silu ? dispatch_mfma<true>(a, c, g.nblocks, st) : dispatch_mfma<false>(a, c, g.nblocks, st);
         } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {
             rc = silu ? dispatch_mfma_lds<true>(a, c, g.nblocks, st) : dispatch_mfma_lds<false>(a, c, g.nblocks, st);
@@ -694,6 +814,71 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx, const void* w, int64_t ldw,
                          int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
                          void* workspace, size_t workspace_bytes, void* stream) {
     return gemm_impl(x, ldx, w, ldw, y, ldy, M, N, K, epilogue, cfg, workspace, workspace_bytes, stream);
+}
+
+int krk_gemm_bf16_normed(const void* x, int64_t ldx, const void* d, int64_t ldd, const void* w_norm, float eps,
+                         void* xout, int64_t ldxo, const void* w, int64_t ldw, void* y, int64_t ldy,
+                         int M, int N, int K, int epilogue, void* workspace, size_t workspace_bytes, void* stream) {
+    const NormSpec ns{d, ldd, w_norm, eps, xout, ldxo};
+    return gemm_impl(x, ldx, w, ldw, y, ldy, M, N, K, epilogue, nullptr, workspace, workspace_bytes, stream, &ns);
+}
+
+int krk_gemm_bf16_normed_config(const void* x, int64_t ldx, const void* d, int64_t ldd, const void* w_norm, float eps,
+                                void* xout, int64_t ldxo, const void* w, int64_t ldw, void* y, int64_t ldy,
+                                int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    const NormSpec ns{d, ldd, w_norm, eps, xout, ldxo};
+    return gemm_impl(x, ldx, w, ldw, y, ldy, M, N, K, epilogue, cfg, workspace, workspace_bytes, stream, &ns);
+}
+
+size_t krk_gemm_normed_workspace_bytes(int M, int N, int K, int epilogue, const krk_gemm_config* cfg) {
+    if (check_shape(M, N, K, epilogue)) return 0;
+    krk_gemm_config c;
+    if (resolve_config(M, N, K, epilogue, cfg, &c)) return 0;
+    return workspace_layout(M, N, K, epilogue, c, true).total;
+}
+
+int krk_gemm_normed_fused(int M, int N, int K, int epilogue, const krk_gemm_config* cfg) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    krk_gemm_config c;
+    if ((rc = resolve_config(M, N, K, epilogue, cfg, &c))) return rc;
+    return norm_fused(M, N, K, epilogue, c) ? 1 : 0;
+}
+
+int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd, const void* w_norm, float eps,
+                          void* xout, int64_t ldxo, void* out, int64_t ldo, int M, int K, void* stream) {
+    g_err[0] = '\0';
+    if (M < 1 || K < 8 || K % 8) return fail(KRK_ERR_INVALID, "shape M=%d K=%d: need M >= 1, K >= 8, K %% 8 == 0", M, K);
+    if (K > krk::kNormThreads * 8 * krk::kNormMaxVec)
+        return fail(KRK_ERR_UNSUPPORTED, "add_rms_norm handles K <= %d, got %d", krk::kNormThreads * 8 * krk::kNormMaxVec, K);
+    if (!x || !d || !w_norm || !xout || !out) return fail(KRK_ERR_INVALID, "null operand pointer");
+    if (ldx < K || ldd < K || ldxo < K || ldo < K) return fail(KRK_ERR_INVALID, "row strides must be >= K=%d", K);
+    if ((ldx | ldd | ldxo | ldo) % 8) return fail(KRK_ERR_ALIGN, "row strides must be multiples of 8 elements");
+    if (((uintptr_t)x | (uintptr_t)d | (uintptr_t)w_norm | (uintptr_t)xout | (uintptr_t)out) % 16)
+        return fail(KRK_ERR_ALIGN, "operands must be 16-byte aligned");
+    if (!(eps >= 0.0f) || eps == __builtin_inff()) return fail(KRK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
+    auto span = [&](const void* p, int64_t ld) {
+        const uintptr_t a = (uintptr_t)p;
+        return std::pair<uintptr_t, uintptr_t>(a, a + ((uint64_t)(M - 1) * ld + K) * 2);
+    };
+    const auto X = span(x, ldx), D = span(d, ldd), XO = span(xout, ldxo), O = span(out, ldo);
+    const uintptr_t g0 = (uintptr_t)w_norm, g1 = g0 + (uint64_t)K * 2;
+    // Each row is read and written by one workgroup, each element by one
+    // thread, so xout may be x itself (the reference's in-place form).
+    const bool in_place = xout == x && ldxo == ldx;
+    if ((!in_place && overlaps(XO.first, XO.second, X.first, X.second)) || overlaps(XO.first, XO.second, D.first, D.second) ||
+        overlaps(XO.first, XO.second, g0, g1) || overlaps(O.first, O.second, X.first, X.second) ||
+        overlaps(O.first, O.second, D.first, D.second) || overlaps(O.first, O.second, g0, g1))
+        return fail(KRK_ERR_ALIAS, "xout and out may not share memory with x (except xout == x), d or w_norm");
+    if (overlaps(XO.first, XO.second, O.first, O.second)) return fail(KRK_ERR_ALIAS, "xout and out may not overlap");
+    krk::NormArgs na{static_cast<const uint16_t*>(d), ldd, static_cast<const uint16_t*>(w_norm), eps,
+                     static_cast<uint16_t*>(xout), ldxo};
+    void* args[] = {(void*)&x, (void*)&ldx, (void*)&na, (void*)&out, (void*)&ldo, (void*)&K};
+    hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&krk::add_rmsnorm_kernel), dim3(M),
+                                   dim3(krk::kNormThreads), args, 0, static_cast<hipStream_t>(stream));
+    return hip_status(e, "add_rmsnorm_kernel launch");
 }
 
 size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue) {

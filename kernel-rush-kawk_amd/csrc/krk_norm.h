@@ -1,0 +1,120 @@
+// Residual add + RMSNorm prologue of the normed projections (gfx950).
+//
+//   xout = bf16(x + d)
+//   n    = bf16( bf16(xout · rstd) · w_norm ),  rstd = 1/sqrt(mean(xout²) + eps)
+//
+// with the mean of squares accumulated in fp32.  These are the rounding points
+// of the reference's fused prologue and of its stand-alone kernel
+// (engine/kernels/gemm.py:21-51 _norm_stats/_normed_tile,
+// engine/kernels/add_rmsnorm.py:15-29, cast placement
+// engine/kernels/rmsnorm.py:34-43: the normalised value rounds to bf16 before
+// the weight multiply).  `d` is the branch output the reference calls `y`.
+//
+// rstd is the correctly rounded fp32 reciprocal square root of the fp32 mean
+// plus eps.  Sums of squares are taken in a fixed order (per thread in k
+// order, then a fixed butterfly, then waves in order), so results are
+// deterministic.
+#pragma once
+
+#include "krk_common.h"
+
+namespace krk {
+
+// Operands of the prologue, passed by value to the kernels that apply it.
+struct NormArgs {
+    const uint16_t* d;   // [M, K] branch output added to x
+    int64_t ldd;
+    const uint16_t* wn;  // [K] RMSNorm gain
+    float eps;
+    uint16_t* xout;      // [M, K] bf16(x + d)
+    int64_t ldxo;
+};
+
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxVec = 8;  // 16-byte vectors per thread: K <= 256 * 8 * 8 = 16384
+
+// bf16 bits of 8 elements a + b (fp32 add, one rounding each).
+__device__ __forceinline__ u32x4 add_bf16x8(const u32x4& a, const u32x4& b) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = f32_to_bf16(bf16_to_f32(a[j] & 0xffffu) + bf16_to_f32(b[j] & 0xffffu));
+        const uint32_t hi = f32_to_bf16(bf16_to_f32(a[j] >> 16) + bf16_to_f32(b[j] >> 16));
+        r[j] = lo | (hi << 16);
+    }
+    return r;
+}
+
+// Sum of squares of 8 bf16 values, in element order, added to acc.
+__device__ __forceinline__ float sumsq_bf16x8(const u32x4& s, float acc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_to_f32(s[j] & 0xffffu);
+        const float hi = bf16_to_f32(s[j] >> 16);
+        acc = __builtin_fmaf(lo, lo, acc);
+        acc = __builtin_fmaf(hi, hi, acc);
+    }
+    return acc;
+}
+
+// bf16 bits of bf16(bf16(s · rstd) · wn) for 8 elements.
+__device__ __forceinline__ u32x4 normalize_bf16x8(const u32x4& s, float rstd, const u32x4& wn) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float lo = round_bf16(bf16_to_f32(s[j] & 0xffffu) * rstd) * bf16_to_f32(wn[j] & 0xffffu);
+        const float hi = round_bf16(bf16_to_f32(s[j] >> 16) * rstd) * bf16_to_f32(wn[j] >> 16);
+        r[j] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+    }
+    return r;
+}
+
+__device__ __forceinline__ float rms_rstd(float sumsq, int K, float eps) {
+    return __frsqrt_rn(sumsq / (float)K + eps);
+}
+
+// Stand-alone prologue: one workgroup per row m writes xout[m] and n[m].
+// Replaces the reference's add_rms_norm launch (engine/kernels/add_rmsnorm.py:32-43)
+// in front of projections that do not fuse it.
+__global__ void __launch_bounds__(kNormThreads)
+add_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t ldx, NormArgs a,
+                   uint16_t* __restrict__ n, int64_t ldn, int K) {
+    __shared__ float red[kNormThreads / 64];
+    const int m = blockIdx.x;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const uint16_t* xr = x + (int64_t)m * ldx;
+    const uint16_t* dr = a.d + (int64_t)m * a.ldd;
+    uint16_t* xo = a.xout + (int64_t)m * a.ldxo;
+    uint16_t* nr = n + (int64_t)m * ldn;
+
+    u32x4 s[kNormMaxVec];
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kNormMaxVec; ++v) {
+        const int k = 8 * (t + kNormThreads * v);
+        if (k < K) {
+            s[v] = add_bf16x8(*reinterpret_cast<const u32x4*>(xr + k), *reinterpret_cast<const u32x4*>(dr + k));
+            *reinterpret_cast<u32x4*>(xo + k) = s[v];
+            ss = sumsq_bf16x8(s[v], ss);
+        }
+    }
+    // Fixed-order reduction: xor butterfly within the wave, then waves in order.
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = red[0];
+#pragma unroll
+    for (int wv = 1; wv < kNormThreads / 64; ++wv) tot += red[wv];
+    const float rstd = rms_rstd(tot, K, a.eps);
+#pragma unroll
+    for (int v = 0; v < kNormMaxVec; ++v) {
+        const int k = 8 * (t + kNormThreads * v);
+        if (k < K)
+            *reinterpret_cast<u32x4*>(nr + k) = normalize_bf16x8(s[v], rstd, *reinterpret_cast<const u32x4*>(a.wn + k));
+    }
+}
+
+}  // namespace krk

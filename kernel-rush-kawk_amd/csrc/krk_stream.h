@@ -249,7 +249,6 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
     int t = 0;
     for (int bi = 0; bi < myblocks; ++bi) {
-        const int b = gi + bi * Gs;
         f32x4 acc[MT];
 #pragma unroll
         for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};

@@ -28,6 +28,7 @@
 #pragma once
 
 #include "krk_epilogue.h"
+#include "krk_norm.h"
 #include "krk_sync.h"
 
 namespace krk {
@@ -40,6 +41,11 @@ constexpr int kValuLdsMinRows = 4;  // x rows from which x is staged in LDS
 // 512-element blocks (none when x stays in registers).
 __host__ __device__ constexpr size_t valu_lds_bytes(int MX, int blocks) {
     return MX < kValuLdsMinRows ? 0 : (size_t)MX * blocks * kValuBlock * sizeof(uint16_t);
+}
+// With the fused RMSNorm prologue: x and the branch rows of the whole K
+// (nb blocks), then the per-wave partial sums of squares.
+__host__ __device__ constexpr size_t valu_norm_lds_bytes(int MX, int nb) {
+    return (size_t)2 * MX * nb * kValuBlock * sizeof(uint16_t) + (size_t)MX * kValuMaxWaves * sizeof(float);
 }
 
 __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
@@ -122,18 +128,22 @@ constexpr int log2_exact() {
 // MX: x rows held (>= M); R: W rows per wave (for SILU R/2 gate rows then the
 // matching R/2 up rows); D: 512-element blocks loaded per row before the wave
 // consumes them; EXACT: K is whole blocks and every split is whole chunks of D
-// blocks, so no load needs clamping and no lane masking.
+// blocks, so no load needs clamping and no lane masking.  NORM: x is the
+// residual stream and the projection input is rms_norm(x + na.d) (krk_norm.h):
+// every workgroup stages x and d for the whole K in LDS, takes the row
+// statistics, and replaces its split's x blocks by the normalised rows;
+// workgroup (0, 0) also writes na.xout.
 // Grid: x = output blocks, y = K splits; blockDim = 64 x waves; each workgroup
 // covers waves * R (SILU: waves * R/2) consecutive output channels.  Split s
 // owns K blocks [s*per + min(s, rem), ...) where per = nb / splits and
 // rem = nb % splits (nb = ceil(K / 512)), so no division runs on the device.
-template <int MX, int R, int D, bool SILU, bool EXACT>
+template <int MX, int R, int D, bool SILU, bool EXACT, bool NORM = false>
 __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w, int64_t ldw,
     uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int per, int rem,
-    float* __restrict__ part, uint32_t* __restrict__ ctr) {
+    float* __restrict__ part, uint32_t* __restrict__ ctr, NormArgs na) {
     static_assert(!SILU || R % 2 == 0, "SILU pairs gate and up rows");
-    constexpr bool XLDS = MX >= kValuLdsMinRows;
+    constexpr bool XLDS = MX >= kValuLdsMinRows || NORM;
     static_assert(((XLDS ? 0 : MX) + R) * D < 64, "vmcnt counts at most 63 loads");
     constexpr int RO = SILU ? R / 2 : R;  // output channels per wave
     constexpr int V = MX * R;
@@ -217,7 +227,9 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
                 u32x4 xb[MX];
 #pragma unroll
                 for (int m = 0; m < MX; ++m) {
-                    if constexpr (XLDS) {
+                    if constexpr (NORM) {
+                        xb[m] = *reinterpret_cast<const u32x4*>(xs + ((size_t)(m * nb + bb) * kValuBlock + lane_k) * 2);
+                    } else if constexpr (XLDS) {
                         xb[m] = *reinterpret_cast<const u32x4*>(
                             xs + ((size_t)(m * (b1 - b0) + (bb - b0)) * kValuBlock + lane_k) * 2);
                     } else {
@@ -249,7 +261,81 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     // registers carried across iterations); the whole K range of a split is
     // usually one chunk.
     int b = b0;
-    if constexpr (XLDS) {
+    if constexpr (NORM) {
+        // x and d rows of the whole K into LDS as [m][block][512] (x, then d),
+        // one 1 KB DMA per (row, block); then the first W loads.
+        unsigned char* const ds = xs + (size_t)MX * nb * kValuBlock * 2;
+        float* const red = reinterpret_cast<float*>(ds + (size_t)MX * nb * kValuBlock * 2);
+        const uint16_t* drow[MX];
+#pragma unroll
+        for (int m = 0; m < MX; ++m) drow[m] = na.d + (int64_t)(m < M ? m : M - 1) * na.ldd;
+        auto kfull = [&](int bb) -> uint32_t {
+            const uint32_t k = (uint32_t)bb * kValuBlock + lane_k;
+            return k < (uint32_t)K ? k : 0u;
+        };
+        for (int j = wave; j < 2 * MX * nb; j += waves) {
+            const int isd = j >= MX * nb;
+            const int jj = isd ? j - MX * nb : j;
+            const int m = jj / nb;
+            const int bb = jj - m * nb;
+            const uint16_t* src = (isd ? drow[m] : xrow[m]) + kfull(bb);
+            dma_row(src, (isd ? ds : xs) + (size_t)jj * (kValuBlock * 2));
+        }
+        issue(b0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        vm_wait<0>();
+        bare_barrier();
+        // Sums of squares of s = bf16(x + d) per row; s replaces x in LDS.
+        const bool write_xout = blockIdx.x == 0 && blockIdx.y == 0;
+        float ss[MX];
+#pragma unroll
+        for (int m = 0; m < MX; ++m) {
+            ss[m] = 0.0f;
+            for (int e = threadIdx.x; e < nb * 64; e += blockDim.x) {
+                const uint32_t k = 8u * (uint32_t)e;
+                if (k < (uint32_t)K) {
+                    unsigned char* px = xs + ((size_t)m * nb * kValuBlock + k) * 2;
+                    const u32x4 sv = add_bf16x8(*reinterpret_cast<const u32x4*>(px),
+                                                *reinterpret_cast<const u32x4*>(ds + ((size_t)m * nb * kValuBlock + k) * 2));
+                    *reinterpret_cast<u32x4*>(px) = sv;
+                    if (write_xout && m < M) *reinterpret_cast<u32x4*>(na.xout + (int64_t)m * na.ldxo + k) = sv;
+                    ss[m] = sumsq_bf16x8(sv, ss[m]);
+                }
+            }
+        }
+        // Fixed-order reduction: butterfly within the wave, waves in order.
+        constexpr int PM = log2_exact<MX>();
+        wave_fold<MX, 32>(ss, lane);
+        {
+            const int v = (lane >> (6 - PM)) & (MX - 1);
+            if ((lane & ((64 >> PM) - 1)) == 0) red[wave * MX + v] = ss[0];
+        }
+        lds_wait();
+        bare_barrier();
+        float rstd[MX];
+#pragma unroll
+        for (int m = 0; m < MX; ++m) {
+            float t = red[m];
+            for (int wv = 1; wv < waves; ++wv) t += red[wv * MX + m];
+            rstd[m] = rms_rstd(t, K, na.eps);
+        }
+        // Normalise this split's blocks in place.
+        for (int e = threadIdx.x; e < (b1 - b0) * 64; e += blockDim.x) {
+            const uint32_t k = (uint32_t)b0 * kValuBlock + 8u * (uint32_t)e;
+            if (k < (uint32_t)K) {
+                const u32x4 g = *reinterpret_cast<const u32x4*>(na.wn + k);
+#pragma unroll
+                for (int m = 0; m < MX; ++m) {
+                    unsigned char* px = xs + ((size_t)m * nb * kValuBlock + k) * 2;
+                    *reinterpret_cast<u32x4*>(px) = normalize_bf16x8(*reinterpret_cast<const u32x4*>(px), rstd[m], g);
+                }
+            }
+        }
+        lds_wait();
+        bare_barrier();
+        consume(b0);
+        b += D;
+    } else if constexpr (XLDS) {
         // x[0:MX, b0*512 : b1*512) into LDS as [m][block][512], one 1 KB DMA
         // per (row, block), spread over the waves; the first W loads go out
         // behind them.  The barrier publishes x after a full vmcnt drain: the

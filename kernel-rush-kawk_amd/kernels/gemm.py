@@ -11,6 +11,9 @@ Python surface of libkrk_gemm.so, shaped like the reference's
 * :func:`pick_matmul` / :func:`pick_gateup` — per-shape callables validated
   at warm-up against ``torch.nn.functional.linear`` on the same device
   (reference pickers, engine/kernels/gemm.py:417-498);
+* ``norm=(y, w_norm, xout, eps)`` on every call, :func:`pick_normed` and
+  :func:`add_rms_norm` — the residual-add + RMSNorm prologue (reference
+  engine/kernels/gemm.py:21-51, 501-560 and engine/kernels/add_rmsnorm.py);
 * :func:`_time` — CUDA/HIP-graph replay timer (engine/kernels/gemm.py:378-414).
 
 All compute runs in the HIP kernels of libkrk_gemm.so; nothing here falls
@@ -29,7 +32,8 @@ from . import _lib
 from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
-    "SkinnyMatmul", "SkinnyGateUp", "Gemv", "pick_matmul", "pick_gateup", "plan", "gemm_into", "_time",
+    "SkinnyMatmul", "SkinnyGateUp", "Gemv", "pick_matmul", "pick_gateup", "pick_normed", "add_rms_norm", "plan",
+    "gemm_into", "normed_fused", "_time",
 ]
 
 
@@ -55,14 +59,33 @@ def _check_operand(name: str, t: torch.Tensor, rows: int | None, cols: int) -> N
         raise ValueError(f"{name} rows must be contiguous (stride(1) == 1), got strides {t.stride()}")
 
 
+def _check_norm(norm, M: int, K: int, device):
+    """Unpack and check ``norm=(y, w_norm, xout, eps)`` (the reference's
+    tuple, engine/kernels/gemm.py:346-350)."""
+    try:
+        d, wn, xout, eps = norm
+    except (TypeError, ValueError):
+        raise ValueError("norm must be a tuple (y, w_norm, xout, eps)") from None
+    _check_operand("norm y", d, M, K)
+    _check_operand("xout", xout, M, K)
+    if not isinstance(wn, torch.Tensor) or wn.dtype != torch.bfloat16 or wn.numel() != K or not wn.is_contiguous():
+        raise ValueError(f"w_norm must be a contiguous bf16 tensor of {K} elements")
+    for name, t in (("norm y", d), ("w_norm", wn), ("xout", xout)):
+        if t.device != device:
+            raise ValueError(f"{name} must be on the operands' device {device}, got {t.device}")
+    return d, wn, xout, float(eps)
+
+
 def gemm_into(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, epilogue: int = EPILOGUE_NONE,
-              workspace: torch.Tensor | None = None, config: dict | None = None) -> torch.Tensor:
+              workspace: torch.Tensor | None = None, config: dict | None = None, norm=None) -> torch.Tensor:
     """Allocation-free call: ``y = epilogue(x @ w.T)`` into the caller's ``y``.
 
     Counterpart of the reference's caller-owned-output launcher
     (``launch_gateup64``, engine/kernels/gateup64.py:59-81).  ``workspace`` must
     hold at least ``workspace_bytes`` bytes of zero-filled device memory when
-    the plan splits K.
+    the plan splits K.  ``norm=(y, w_norm, xout, eps)`` fuses
+    ``xout = x + y; x = rms_norm(xout, w_norm)`` in front, as the reference's
+    ``norm`` argument does (engine/kernels/gemm.py:346-361).
     """
     M, K = x.shape
     N = w.shape[0]
@@ -75,6 +98,8 @@ def gemm_into(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, epilogue: int =
             raise ValueError(f"{name} must be a GPU tensor, got device {t.device}")
     if not (x.device == w.device == y.device):
         raise ValueError(f"operands on different devices: {x.device}, {w.device}, {y.device}")
+    if norm is not None:
+        d, wn, xout, eps = _check_norm(norm, M, K, x.device)
     ws_ptr, ws_bytes = 0, 0
     if workspace is not None:
         if workspace.device != x.device:
@@ -82,24 +107,64 @@ def gemm_into(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, epilogue: int =
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     lib = _lib.load()
+    cfg = GemmConfig.from_dict(config) if config is not None else None
     with torch.cuda.device(x.device):
-        if config is None:
+        if norm is not None:
+            head = (x.data_ptr(), x.stride(0), d.data_ptr(), d.stride(0), wn.data_ptr(), eps, xout.data_ptr(),
+                    xout.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0), M, N, K, epilogue)
+            if cfg is None:
+                rc = lib.krk_gemm_bf16_normed(*head, ws_ptr, ws_bytes, stream)
+            else:
+                rc = lib.krk_gemm_bf16_normed_config(*head, ctypes.byref(cfg), ws_ptr, ws_bytes, stream)
+        elif cfg is None:
             rc = lib.krk_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0),
                                    M, N, K, epilogue, ws_ptr, ws_bytes, stream)
         else:
-            cfg = GemmConfig.from_dict(config)
             rc = lib.krk_gemm_bf16_config(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
                                           y.stride(0), M, N, K, epilogue, ctypes.byref(cfg), ws_ptr, ws_bytes, stream)
     _lib.check(rc)
     return y
 
 
-def workspace_bytes(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE, config: dict | None = None) -> int:
+def workspace_bytes(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE, config: dict | None = None,
+                    normed: bool = False) -> int:
     lib = _lib.load()
+    if normed:
+        cfg = GemmConfig.from_dict(config) if config is not None else None
+        return int(lib.krk_gemm_normed_workspace_bytes(M, N, K, epilogue, ctypes.byref(cfg) if cfg else None))
     if config is None:
         return int(lib.krk_gemm_workspace_bytes(M, N, K, epilogue))
     cfg = GemmConfig.from_dict(config)
     return int(lib.krk_gemm_config_workspace_bytes(M, N, K, epilogue, ctypes.byref(cfg)))
+
+
+def normed_fused(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE, config: dict | None = None) -> bool:
+    """Whether a normed call of this shape runs the prologue inside the
+    projection kernel (one launch) rather than as a separate kernel."""
+    cfg = GemmConfig.from_dict(config) if config is not None else None
+    rc = _lib.load().krk_gemm_normed_fused(M, N, K, epilogue, ctypes.byref(cfg) if cfg else None)
+    if rc < 0:
+        _lib.check(rc)
+    return rc == 1
+
+
+def add_rms_norm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, eps: float,
+                 xout: torch.Tensor | None = None) -> torch.Tensor:
+    """``xout = x + y`` (bf16; in place into ``x`` when ``xout`` is None) and
+    return ``rms_norm(xout, weight)`` — the reference's stand-alone kernel
+    (engine/kernels/add_rmsnorm.py:32-43), on libkrk_gemm.so."""
+    M, K = x.shape
+    _check_operand("x", x, None, K)
+    xo = x if xout is None else xout
+    d, wn, xo, eps = _check_norm((y, weight, xo, eps), M, K, x.device)
+    out = torch.empty_like(x)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    with torch.cuda.device(x.device):
+        rc = _lib.load().krk_add_rms_norm_bf16(x.data_ptr(), x.stride(0), d.data_ptr(), d.stride(0), wn.data_ptr(),
+                                               eps, xo.data_ptr(), xo.stride(0), out.data_ptr(), out.stride(0), M, K,
+                                               stream)
+    _lib.check(rc)
+    return out
 
 
 class SkinnyMatmul:
@@ -121,7 +186,10 @@ class SkinnyMatmul:
         self.config = dict(config) if config else None
         # An invalid explicit config also reports 0 here; the first call then
         # raises ValueError with the library's explanation.
-        nbytes = workspace_bytes(M, N, K, self.epilogue, self.config)
+        # One workspace serves plain and normed calls: both keep their split-K
+        # counters at its start; normed calls may use more of it as scratch.
+        nbytes = max(workspace_bytes(M, N, K, self.epilogue, self.config),
+                     workspace_bytes(M, N, K, self.epilogue, self.config, normed=True))
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device) if nbytes else None
         self.out_cols = N // 2 if self.epilogue == EPILOGUE_SILU_MUL else N
 
@@ -131,16 +199,18 @@ class SkinnyMatmul:
             return plan(self.M, self.N, self.K, self.epilogue)
         return dict(self.config)
 
-    def run(self, a: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    def run(self, a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, norm=None) -> torch.Tensor:
         """Allocation-free form: write into ``out``."""
         if a.shape[0] != self.M or a.shape[1] != self.K or w.shape[0] != self.N:
             raise ValueError(f"operands {tuple(a.shape)} x {tuple(w.shape)} do not match the "
                              f"({self.M}, {self.N}, {self.K}) this object was built for")
-        return gemm_into(a, w, out, self.epilogue, self.workspace, self.config)
+        return gemm_into(a, w, out, self.epilogue, self.workspace, self.config, norm)
 
-    def __call__(self, a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, norm=None) -> torch.Tensor:
+        """``norm=(y, w_norm, xout, eps)`` fuses ``xout = a + y; a = rms_norm(xout, w_norm)``
+        in front (reference signature, engine/kernels/gemm.py:346-347)."""
         out = torch.empty((self.M, self.out_cols), dtype=torch.bfloat16, device=a.device)
-        return self.run(a, w, out)
+        return self.run(a, w, out, norm)
 
 
 class SkinnyGateUp(SkinnyMatmul):
@@ -159,9 +229,9 @@ class SkinnyGateUp(SkinnyMatmul):
         self.I = I
         super().__init__(M, 2 * I, K, device, config)
 
-    def __call__(self, a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor | None = None) -> torch.Tensor:
+    def __call__(self, a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor | None = None, norm=None) -> torch.Tensor:
         wgu = wg if wu is None else _join_halves(wg, wu, self.I)
-        return super().__call__(a, wgu)
+        return super().__call__(a, wgu, norm)
 
 
 def _join_halves(wg: torch.Tensor, wu: torch.Tensor, I: int) -> torch.Tensor:
@@ -185,10 +255,10 @@ class Gemv(SkinnyMatmul):
         super().__init__(M, 2 * N if gateup else N, K, device, config)
         self.I = N
 
-    def __call__(self, a: torch.Tensor, w: torch.Tensor, w2: torch.Tensor | None = None) -> torch.Tensor:
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, w2: torch.Tensor | None = None, norm=None) -> torch.Tensor:
         if self.epilogue == EPILOGUE_SILU_MUL:
             w = w if w2 is None else _join_halves(w, w2, self.I)
-        return super().__call__(a, w)
+        return super().__call__(a, w, norm)
 
 
 def _time(fn, iters: int = 30, rotate: list | None = None) -> float:
@@ -281,3 +351,41 @@ def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = 
         log(f"gateup M={M} I={I} K={K}: krk{mm.resolved_config} {ms * 1000:.1f}us "
             f"({2 * I * K * 2 / ms / 1e6:.0f} GB/s)")
     return mm
+
+
+def _add_rms_norm_ref(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, eps: float):
+    """Torch composition of the prologue (validation reference): the
+    reference's rounding points (engine/kernels/add_rmsnorm.py:20-29)."""
+    s = (x.float() + y.float()).to(torch.bfloat16)
+    sf = s.float()
+    rstd = torch.rsqrt((sf * sf).mean(dim=-1, keepdim=True) + eps)
+    return s, ((sf * rstd).to(torch.bfloat16).float() * w_norm.float()).to(torch.bfloat16)
+
+
+def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, w: torch.Tensor, eps: float,
+                log=None, ws: list | None = None):
+    """Return ``f(x, y, w_norm, xout, w) -> proj(rms_norm(x + y))`` that also
+    writes ``xout = x + y`` (reference engine/kernels/gemm.py:501-560).
+    ``kind`` is "matmul" or "gateup".  Validated once against the torch
+    composition (xout bit-exact, projection within the reference's
+    ``0.02·max|ref| + 1e-3``); with ``log`` the graph-replay time is logged."""
+    if kind not in ("matmul", "gateup"):
+        raise ValueError(f"kind must be 'matmul' or 'gateup', got {kind!r}")
+    M, K = x.shape
+    N = w.shape[0]
+    mm = SkinnyGateUp(M, N // 2, K, x.device) if kind == "gateup" else SkinnyMatmul(M, N, K, x.device)
+    fn = lambda x_, y_, wn_, xout_, w_: mm(x_, w_, norm=(y_, wn_, xout_, eps))
+    xout = torch.empty_like(x)
+    out = fn(x, y, w_norm, xout, w)
+    ref_xout, n = _add_rms_norm_ref(x, y, w_norm, eps)
+    ref = _linear_fp32acc(n, w)
+    if kind == "gateup":
+        ref = _silu_mul(ref)
+    if not torch.equal(xout, ref_xout):
+        raise RuntimeError(f"normed {kind} M={M} N={N} K={K}: xout differs from x + y")
+    _validate(out, ref, f"normed {kind} M={M} N={N} K={K}", log)
+    if log:
+        ms = _time(lambda w_: fn(x, y, w_norm, xout, w_), rotate=ws or [w])
+        fused = "fused" if normed_fused(M, N, K, mm.epilogue) else "prologue kernel"
+        log(f"normed {kind} M={M} N={N} K={K}: krk{mm.resolved_config} ({fused}) {ms * 1000:.1f}us")
+    return fn

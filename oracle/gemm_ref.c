@@ -13,6 +13,10 @@
  *   - SwiGLU epilogue with three bf16 roundings:
  *       engine/kernels/gemm.py:107-113 (_swiglu_epilogue),
  *       engine/kernels/swiglu.py:14-24 (gate-first [M, 2I] layout).
+ *   - residual add + RMSNorm prologue: xout = bf16(x + y),
+ *       n = bf16(bf16(xout·rsqrt(mean(xout²) + eps))·w_norm):
+ *       engine/kernels/add_rmsnorm.py:15-29, engine/kernels/gemm.py:21-51,
+ *       cast placement engine/kernels/rmsnorm.py:34-43.
  *   - token selection: first index of the maximum
  *       (engine/engine.py:196 `argmax`, OPTIMIZATION_GUIDE.md:213 lowest index).
  *
@@ -137,5 +141,31 @@ void oracle_argmax_rows(const uint16_t* v, int64_t ld, int M, int N, int64_t* id
             if (f > bv) { bv = f; best = n; }
         }
         idx[m] = best;
+    }
+}
+
+/* Residual add + RMSNorm over rows of K: xout = bf16(x + y); the mean of
+ * squares of xout is taken in fp64 (any fp32 order lies within a few ulp of
+ * it) and rstd = 1/sqrt(mean + eps) is rounded to fp32, the precision the
+ * reference computes it in; n = bf16(bf16(xout·rstd)·w_norm) with both
+ * products in fp32.  rstd_out receives the fp64 value for error analysis. */
+void oracle_add_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy,
+                         const uint16_t* w_norm, double eps, uint16_t* xout, uint16_t* n, int64_t ldo,
+                         int M, int K, double* rstd_out) {
+    for (int m = 0; m < M; ++m) {
+        double ss = 0.0;
+        for (int k = 0; k < K; ++k) {
+            const uint16_t s = f32_to_bf16(bf16_to_f32(x[m * ldx + k]) + bf16_to_f32(y[m * ldy + k]));
+            xout[m * ldo + k] = s;
+            const double sf = bf16_to_f32(s);
+            ss += sf * sf;
+        }
+        const double rstd = 1.0 / sqrt(ss / K + eps);
+        rstd_out[m] = rstd;
+        const float r32 = (float)rstd;
+        for (int k = 0; k < K; ++k) {
+            const float a = bf16_to_f32(f32_to_bf16(bf16_to_f32(xout[m * ldo + k]) * r32));
+            n[m * ldo + k] = f32_to_bf16(a * bf16_to_f32(w_norm[k]));
+        }
     }
 }

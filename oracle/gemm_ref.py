@@ -67,6 +67,37 @@ def gateup_bf16(x: torch.Tensor, wgu: torch.Tensor) -> torch.Tensor:
     return swiglu_bf16(linear_bf16(x, wgu))
 
 
+def add_rms_norm_bf16(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, eps: float):
+    """Residual add + RMSNorm with the reference's rounding points: returns
+    ``(xout, n)`` with ``xout = bf16(x + y)`` and
+    ``n = bf16(bf16(xout · rsqrt(mean(xout²) + eps)) · w_norm)``, the mean of
+    squares accumulated in fp32.  Reference: engine/kernels/add_rmsnorm.py:15-29
+    (``add_rms_norm``), engine/kernels/gemm.py:21-51 (``_norm_stats`` and
+    ``_normed_tile``, the fused prologue), cast placement per
+    engine/kernels/rmsnorm.py:34-43."""
+    x = x.detach().to("cpu", torch.bfloat16).float()
+    y = y.detach().to("cpu", torch.bfloat16).float()
+    wn = w_norm.detach().to("cpu", torch.bfloat16).float()
+    s = (x + y).to(torch.bfloat16)
+    sf = s.float()
+    rstd = torch.rsqrt((sf * sf).sum(dim=-1, keepdim=True) / sf.shape[-1] + eps)
+    n = (sf * rstd).to(torch.bfloat16).float() * wn
+    return s, n.to(torch.bfloat16)
+
+
+def normed_linear_bf16(x, y, w_norm, eps, w):
+    """``(xout, n @ w.T)``: the pick_normed contract for "matmul"
+    (engine/kernels/gemm.py:501-560, engine/model.py:166)."""
+    xout, n = add_rms_norm_bf16(x, y, w_norm, eps)
+    return xout, linear_bf16(n, w)
+
+
+def normed_gateup_bf16(x, y, w_norm, eps, wgu):
+    """``(xout, swiglu(n @ wgu.T))``: the pick_normed contract for "gateup"."""
+    xout, n = add_rms_norm_bf16(x, y, w_norm, eps)
+    return xout, gateup_bf16(n, wgu)
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     """Per-row index of the maximum, lowest index on ties (torch.argmax
     returns the first occurrence).  Reference: engine/engine.py:196."""
@@ -180,6 +211,7 @@ def c_lib() -> ctypes.CDLL:
         lib.oracle_swiglu.argtypes = [P, i64, P, i64, i32, i32]
         lib.oracle_gateup_f32.argtypes = [P, i64, P, i64, P, i64, i32, i32, i32]
         lib.oracle_argmax_rows.argtypes = [P, i64, i32, i32, P]
+        lib.oracle_add_rms_norm.argtypes = [P, i64, P, i64, P, ctypes.c_double, P, P, i64, i32, i32, P]
         _C = lib
     return _C
 
@@ -233,6 +265,18 @@ def c_argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     idx = np.empty((M,), np.int64)
     c_lib().oracle_argmax_rows(_ptr(b), N, M, N, _ptr(idx))
     return torch.from_numpy(idx)
+
+
+def c_add_rms_norm(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, eps: float):
+    """(xout, n, rstd fp64) from the C restatement: statistics in fp64, the
+    same three bf16 rounding points."""
+    xb, yb, wb = to_bits(x), to_bits(y), to_bits(w_norm.reshape(1, -1))
+    M, K = xb.shape
+    xo = np.empty((M, K), np.uint16)
+    n = np.empty((M, K), np.uint16)
+    rstd = np.empty((M,), np.float64)
+    c_lib().oracle_add_rms_norm(_ptr(xb), K, _ptr(yb), K, _ptr(wb), float(eps), _ptr(xo), _ptr(n), K, M, K, _ptr(rstd))
+    return from_bits(xo), from_bits(n), rstd
 
 
 # --------------------------------------------------------------------------

@@ -230,3 +230,76 @@ def test_error_mapping():
     with pytest.raises(_lib.KrkError):
         _lib.check(_lib.KRK_ERR_HIP)
     _lib.check(_lib.KRK_OK)
+
+
+# ------------------------------------------------------------------ normed projections
+
+D, G, XO = 0x50000000, 0x60000000, 0x70000000
+
+
+def call_normed(lib, x=X, ldx=2560, d=D, ldd=2560, g=G, eps=1e-6, xo=XO, ldxo=2560, w=W, ldw=2560, y=Y, ldy=None,
+                M=1, N=6144, K=2560, epi=NONE, ws=WS, wsb=1 << 30):
+    if ldy is None:
+        ldy = N // 2 if epi == SILU else N
+    return lib.krk_gemm_bf16_normed(x, ldx, d, ldd, g, eps, xo, ldxo, w, ldw, y, ldy, M, N, K, epi, ws, wsb, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(d=0), _lib.KRK_ERR_INVALID, "null norm operand"),
+    (dict(xo=0), _lib.KRK_ERR_INVALID, "null norm operand"),
+    (dict(ldd=2552), _lib.KRK_ERR_INVALID, "ldd"),
+    (dict(ldxo=2561), _lib.KRK_ERR_ALIGN, "multiples of 8"),
+    (dict(d=D + 8), _lib.KRK_ERR_ALIGN, "16-byte aligned"),
+    (dict(g=G + 2), _lib.KRK_ERR_ALIGN, "16-byte aligned"),
+    (dict(eps=-1.0), _lib.KRK_ERR_INVALID, "eps"),
+    (dict(eps=float("nan")), _lib.KRK_ERR_INVALID, "eps"),
+    (dict(xo=X), _lib.KRK_ERR_ALIAS, "xout may not share"),
+    (dict(xo=D + 1024), _lib.KRK_ERR_ALIAS, "xout may not share"),
+    (dict(y=D), _lib.KRK_ERR_ALIAS, "may not share"),
+    (dict(K=16392, ldx=16392, ldd=16392, ldxo=16392, ldw=16392), _lib.KRK_ERR_UNSUPPORTED, "K <="),
+    (dict(ws=0, M=32), _lib.KRK_ERR_WORKSPACE, "workspace"),
+    (dict(ws=XO, M=32), _lib.KRK_ERR_ALIAS, "workspace may not share"),
+])
+def test_normed_argument_errors(lib, kw, code, msg):
+    assert call_normed(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_normed_fused_only_at_m1_with_a_modest_grid(lib):
+    """M = 1 VALU plans of up to 2048 workgroups fuse the prologue (qkv,
+    gate_up); lm_head's 19k-workgroup plan and every M > 1 run the separate
+    prologue kernel."""
+    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["gate_up"], 1, 1), (QWEN["qkv"], 4, 0),
+                                  (QWEN["gate_up"], 8, 0), (QWEN["lm_head"], 1, 0), (QWEN["qkv"], 32, 0),
+                                  (QWEN["gate_up"], 32, 0), (QWEN["lm_head"], 64, 0)]:
+        assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == fused, (N, M)
+    assert lib.krk_gemm_normed_fused(0, 6144, 2560, NONE, None) == _lib.KRK_ERR_INVALID
+
+
+def test_normed_workspace_adds_the_normalised_rows(lib):
+    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["gate_up"], 64), (QWEN["lm_head"], 17), (QWEN["qkv"], 100)]:
+        plain = lib.krk_gemm_workspace_bytes(M, N, K, epi)
+        normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None)
+        assert normed == -(-plain // 256) * 256 + M * K * 2
+    for (N, K, epi), M in [(QWEN["qkv"], 1), (QWEN["gate_up"], 1)]:
+        assert lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None) == lib.krk_gemm_workspace_bytes(M, N, K, epi)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=0), _lib.KRK_ERR_INVALID),
+    (dict(K=12), _lib.KRK_ERR_INVALID),
+    (dict(eps=-2.0), _lib.KRK_ERR_INVALID),
+    (dict(xo=D), _lib.KRK_ERR_ALIAS),
+    (dict(out=X + 64), _lib.KRK_ERR_ALIAS),
+    (dict(out=XO), _lib.KRK_ERR_ALIAS),
+    (dict(xo=X, ldxo=2568), _lib.KRK_ERR_ALIAS),
+    (dict(K=16392, ldx=16392, ldd=16392, ldxo=16392, ldo=16392), _lib.KRK_ERR_UNSUPPORTED),
+])
+def test_add_rms_norm_argument_errors(lib, kw, code):
+    a = dict(x=X, ldx=2560, d=D, ldd=2560, g=G, eps=1e-6, xo=XO, ldxo=2560, out=Y, ldo=2560, M=4, K=2560)
+    a.update(kw)
+    if "ldx" not in kw and a["K"] > 2560:
+        a["ldx"] = a["K"]
+    rc = lib.krk_add_rms_norm_bf16(a["x"], a["ldx"], a["d"], a["ldd"], a["g"], a["eps"], a["xo"], a["ldxo"],
+                                   a["out"], a["ldo"], a["M"], a["K"], None)
+    assert rc == code, _lib.last_error()

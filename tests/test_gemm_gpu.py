@@ -496,3 +496,152 @@ def test_pickers_return_validated_callables(device):
     assert_parity(gu(a, wgu).cpu(), R.gateup_bf16(a, wgu), "pick_gateup")
     assert_parity(gu(a, wgu[:9728], wgu[9728:]).cpu(), R.gateup_bf16(a, wgu), "pick_gateup halves")
     assert any("us" in l for l in logs)
+
+
+# ------------------------------------------------------------------ normed projections (RMSNorm prologue)
+
+EPS = 1e-6
+#: (K, N, epilogue) of the normed projections (their input is rms_norm(x + y)).
+QWEN = {"qkv": (2560, 6144, NONE), "gate_up": (2560, 19456, SILU), "lm_head": (2560, 151936, NONE)}
+
+
+def krk_normed(x, y, wn, w, epilogue=NONE, config=None, device="cuda:0"):
+    """Normed HIP call on CPU bf16 inputs; returns (xout, out) on the CPU."""
+    M, K = x.shape
+    N = w.shape[0]
+    nout = N // 2 if epilogue == SILU else N
+    xd, yd, gd, wd = x.to(device), y.to(device), wn.to(device), w.to(device)
+    out = torch.empty((M, nout), dtype=torch.bfloat16, device=device)
+    xout = torch.empty((M, K), dtype=torch.bfloat16, device=device)
+    nbytes = G.workspace_bytes(M, N, K, epilogue, config, normed=True)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+    G.gemm_into(xd, wd, out, epilogue, ws, config, norm=(yd, gd, xout, EPS))
+    torch.cuda.synchronize()
+    return xout.cpu(), out.cpu()
+
+
+def _norm_inputs(M, K, seed):
+    return (R.randn_bf16((M, K), seed), R.randn_bf16((M, K), seed + 1, 0.5), R.randn_bf16((K,), seed + 2))
+
+
+def _check_normed(x, y, wn, w, epi, got_xout, got, what):
+    ref_xout, ref = (R.normed_gateup_bf16 if epi == SILU else R.normed_linear_bf16)(x, y, wn, EPS, w)
+    assert torch.equal(got_xout, ref_xout), f"{what}: xout differs from bf16(x + y)"
+    assert_parity(got, ref, what)
+
+
+@pytest.mark.parametrize("shape,M", [("qkv", M) for M in (1, 2, 3, 4, 8, 9, 32, 64)] +
+                                    [("gate_up", M) for M in (1, 2, 5, 8, 16, 32, 64)] +
+                                    [("lm_head", M) for M in (1, 4, 8, 32)])
+def test_normed_qwen_shapes(device, shape, M):
+    K, N, epi = QWEN[shape]
+    x, y, wn = _norm_inputs(M, K, 9300 + M)
+    w = R.randn_bf16((N, K), 9310 + M, 0.02)
+    say("normed", shape, M, "fused" if G.normed_fused(M, N, K, epi) else "prologue")
+    xo, out = krk_normed(x, y, wn, w, epi)
+    _check_normed(x, y, wn, w, epi, xo, out, f"normed {shape} M={M}")
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(1, 6144, 2560, NONE), (1, 19456, 2560, SILU), (1, 520, 2056, NONE),
+                                       (1, 96, 1000, SILU), (4, 6144, 2560, NONE), (7, 96, 1000, SILU)])
+def test_normed_fused_and_prologue_paths_agree(device, M, N, K, epi):
+    """The fused VALU prologue (every W-rows-per-wave choice, split and
+    unsplit K, ragged K), the VALU plan behind the prologue kernel, and an
+    MFMA plan behind it are all within tolerance of the oracle, and the fused
+    call is deterministic."""
+    x, y, wn = _norm_inputs(M, K, 9400 + M)
+    w = R.randn_bf16((N, K), 9410, 0.02)
+    cfgs = [dict(kernel=_lib.KERNEL_VALU, unroll=5, n_tiles=nt, splits=sp) for nt in (1, 2, 4) for sp in (1, 2)]
+    cfgs += [dict(kernel=_lib.KERNEL_VALU, unroll=2, splits=1), dict(kernel=_lib.KERNEL_MFMA_LDS, splits=1)]
+    ran = 0
+    for cfg in cfgs:
+        try:
+            fused = G.normed_fused(M, N, K, epi, cfg)
+        except ValueError:
+            continue
+        say("normed config", M, N, K, epi, cfg, fused)
+        xo, out = krk_normed(x, y, wn, w, epi, cfg)
+        _check_normed(x, y, wn, w, epi, xo, out, f"normed {cfg}")
+        if fused:
+            assert torch.equal(out, krk_normed(x, y, wn, w, epi, cfg)[1])
+        ran += 1
+    assert ran >= 3
+
+
+def test_normed_rows_beyond_64(device):
+    M, N, K = 100, 384, 2560
+    x, y, wn = _norm_inputs(M, K, 9500)
+    w = R.randn_bf16((N, K), 9501, 0.02)
+    xo, out = krk_normed(x, y, wn, w)
+    _check_normed(x, y, wn, w, NONE, xo, out, "normed M=100")
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (7, 512), (64, 2560), (3, 16384), (5, 2056)])
+def test_add_rms_norm_kernel(device, M, K):
+    x, y, wn = _norm_inputs(M, K, 9600 + M)
+    ref_xo, ref_n = R.add_rms_norm_bf16(x, y, wn, EPS)
+    xd = x.to(device)
+    out = G.add_rms_norm(xd, y.to(device), wn.to(device), EPS, xout=torch.empty_like(xd))
+    xo2 = xd.clone()
+    out_inplace = G.add_rms_norm(xo2, y.to(device), wn.to(device), EPS)  # xout = x (in place)
+    torch.cuda.synchronize()
+    assert torch.equal(xo2.cpu(), ref_xo)
+    for got in (out.cpu(), out_inplace.cpu()):
+        gb, rb = R.to_bits(got).astype(np.int32), R.to_bits(ref_n).astype(np.int32)
+        assert np.abs(gb - rb).max() <= 1 and (gb == rb).mean() > 0.999
+    assert torch.equal(out.cpu(), out_inplace.cpu())
+
+
+def test_normed_graph_replay(device):
+    """Fused and prologue-kernel normed calls captured in one graph replay to
+    the eager results, with eager work between replays."""
+    cases = [(1, 6144, 2560, NONE), (8, 19456, 2560, SILU), (32, 6144, 2560, NONE)]
+    ops, ins, eager, outs = [], [], [], []
+    for i, (M, N, K, epi) in enumerate(cases):
+        op = G.SkinnyGateUp(M, N // 2, K, device) if epi == SILU else G.SkinnyMatmul(M, N, K, device)
+        x, y, wn = (t.to(device) for t in _norm_inputs(M, K, 9700 + i))
+        w = R.randn_bf16((N, K), 9710 + i, 0.02).to(device)
+        xo = torch.empty_like(x)
+        ops.append(op)
+        ins.append((x, y, wn, w, xo))
+        eager.append(op(x, w, norm=(y, wn, xo, EPS)).clone())
+        outs.append(torch.empty_like(eager[-1]))
+    torch.cuda.synchronize()
+    say("normed graph", cases)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for op, (x, y, wn, w, xo), o in zip(ops, ins, outs):
+            op.run(x, w, o, norm=(y, wn, xo, EPS))
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for op, (x, y, wn, w, xo), o in zip(ops, ins, outs):
+            op.run(x, w, o, norm=(y, wn, xo, EPS))
+    for rep in range(3):
+        for o in outs:
+            o.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for e, o in zip(eager, outs):
+            assert torch.equal(e, o), f"normed replay {rep} differs from eager"
+        _ = ops[0](ins[0][0], ins[0][3])  # eager plain call between replays shares the workspace
+        torch.cuda.synchronize()
+
+
+def test_pick_normed_returns_validated_callable(device):
+    M, K, N = 4, 2560, 6144
+    x, y, wn = (t.to(device) for t in _norm_inputs(M, K, 9800))
+    w = R.randn_bf16((N, K), 9801, 0.02).to(device)
+    logs = []
+    f = G.pick_normed("matmul", x, y, wn, w, EPS, log=logs.append)
+    xo = torch.empty_like(x)
+    out = f(x, y, wn, xo, w)
+    torch.cuda.synchronize()
+    _check_normed(x.cpu(), y.cpu(), wn.cpu(), w.cpu(), NONE, xo.cpu(), out.cpu(), "pick_normed")
+    assert any("normed matmul" in l for l in logs)
+    wgu = R.randn_bf16((2 * 9728, K), 9802, 0.02).to(device)
+    g = G.pick_normed("gateup", x, y, wn, wgu, EPS)
+    assert g(x, y, wn, xo, wgu).shape == (M, 9728)

@@ -208,3 +208,77 @@ def test_seeded_inputs_reproducible():
     c = R.randn_bf16((3, 100), 8, 0.02)
     assert torch.equal(a, b) and not torch.equal(a, c)
     assert R.seed_for(4, 35, "down") == 4354
+
+
+# ------------------------------------------------------------------ add + RMSNorm prologue
+
+def _bf16(t):
+    return t.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("which", ["torch", "c"])
+def test_rms_norm_closed_form_constant_row(which):
+    """x = 2, y = 0, eps = 0: mean(xout²) = 4 exactly, rstd = 0.5, xout·rstd = 1,
+    so n must equal w_norm bit for bit (a dropped /K or a wrong sqrt fails)."""
+    K = 2560
+    x = torch.full((3, K), 2.0, dtype=torch.bfloat16)
+    y = torch.zeros((3, K), dtype=torch.bfloat16)
+    wn = R.randn_bf16((K,), 321)
+    xo, n = (R.add_rms_norm_bf16(x, y, wn, 0.0) if which == "torch" else R.c_add_rms_norm(x, y, wn, 0.0)[:2])
+    assert torch.equal(xo, x)
+    assert torch.equal(n, wn.expand(3, K))
+
+
+def test_rms_norm_cancelling_branch_gives_zero():
+    x = R.randn_bf16((2, 512), 11)
+    xo, n = R.add_rms_norm_bf16(x, -x, R.randn_bf16((512,), 12), 1e-6)
+    assert torch.equal(xo.float(), torch.zeros(2, 512)) and torch.equal(n.float(), torch.zeros(2, 512))
+
+
+def test_rms_norm_torch_and_c_restatements_agree():
+    """xout bit-exact; n identical except where the fp32 vs fp64 sum of squares
+    moves rstd by an ulp, and then by at most one bf16 ulp."""
+    M, K = 5, 2560
+    x, y, wn = R.randn_bf16((M, K), 31), R.randn_bf16((M, K), 32, 0.5), R.randn_bf16((K,), 33)
+    xo_t, n_t = R.add_rms_norm_bf16(x, y, wn, 1e-6)
+    xo_c, n_c, _ = R.c_add_rms_norm(x, y, wn, 1e-6)
+    assert torch.equal(xo_t, xo_c)
+    bt, bc = R.to_bits(n_t).astype(np.int32), R.to_bits(n_c).astype(np.int32)
+    assert np.abs(bt - bc).max() <= 1
+    assert (bt == bc).mean() > 0.999
+
+
+def test_rms_norm_rounds_before_the_gain():
+    """The normalised value is rounded to bf16 before the gain multiply
+    (engine/kernels/rmsnorm.py:34-43); rounding once at the end is a different
+    function and must be told apart on random data."""
+    M, K = 4, 2560
+    x, y, wn = R.randn_bf16((M, K), 41), R.randn_bf16((M, K), 42), R.randn_bf16((K,), 43)
+    xo, n = R.add_rms_norm_bf16(x, y, wn, 1e-6)
+    sf = xo.float()
+    rstd = torch.rsqrt((sf * sf).mean(-1, keepdim=True) + 1e-6)
+    once = (sf * rstd * wn.float()).to(torch.bfloat16)
+    assert not torch.equal(once, n)
+    twice = ((sf * rstd).to(torch.bfloat16).float() * wn.float()).to(torch.bfloat16)
+    assert torch.equal(twice, n)
+
+
+def test_rms_norm_scale_invariance():
+    """With eps = 0, scaling x and y by a power of two scales xout exactly and
+    leaves n unchanged."""
+    M, K = 3, 1024
+    x, y, wn = R.randn_bf16((M, K), 51), R.randn_bf16((M, K), 52), R.randn_bf16((K,), 53)
+    xo1, n1 = R.add_rms_norm_bf16(x, y, wn, 0.0)
+    xo4, n4 = R.add_rms_norm_bf16(_bf16(x.float() * 4), _bf16(y.float() * 4), wn, 0.0)
+    assert torch.equal(xo4.float(), xo1.float() * 4)
+    bits1, bits4 = R.to_bits(n1).astype(np.int32), R.to_bits(n4).astype(np.int32)
+    assert np.abs(bits1 - bits4).max() <= 1 and (bits1 == bits4).mean() > 0.999
+
+
+def test_normed_linear_composes_prologue_and_projection():
+    M, K, N = 2, 256, 40
+    x, y, wn, w = R.randn_bf16((M, K), 61), R.randn_bf16((M, K), 62), R.randn_bf16((K,), 63), R.randn_bf16((N, K), 64, 0.02)
+    xo, out = R.normed_linear_bf16(x, y, wn, 1e-6, w)
+    assert torch.equal(out, R.linear_bf16(R.add_rms_norm_bf16(x, y, wn, 1e-6)[1], w))
+    xo2, out2 = R.normed_gateup_bf16(x, y, wn, 1e-6, R.randn_bf16((2 * N, K), 65, 0.02))
+    assert torch.equal(xo, xo2) and out2.shape == (M, N)
