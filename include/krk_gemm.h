@@ -214,6 +214,48 @@ int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd
                           void* out, int64_t ldo, int M, int K, void* stream);
 
 /*
+ * krk_gemm_bf16_select — the lm_head projection with token selection fused:
+ * idx[m][0..k) = indices of the k largest bf16 logits bf16(x[m]·W[n]ᵀ) of
+ * row m, largest first, equal values at the lower index first (NaN above
+ * +inf, -0 equal to +0), without a second launch and without writing the
+ * logits unless y is given.
+ *
+ * Replaces `logits.argmax(dim=-1)` (k = 1; engine/engine.py:196,
+ * engine/model.py:365; lowest index on ties, OPTIMIZATION_GUIDE.md:213) and
+ * `torch.topk(logits, k).indices` (engine/recycle.py:170, k = 8) after the
+ * lm_head call of engine/model.py:209.
+ *
+ *   x, w, M, N, K   as krk_gemm_bf16 (plain epilogue)
+ *   y               [M, N] bf16 logits, stride ldy >= N, or NULL to skip them
+ *   k               1..8 (<= N)
+ *   idx             [M, k] int64 output (-1 past N), 8-byte aligned
+ *   vals            [M, k] bf16 values of the selected logits (a NaN as the
+ *                   canonical quiet NaN 0x7fc0), or NULL
+ *   workspace       krk_gemm_select_workspace_bytes(M, N, K, k, NULL) bytes,
+ *                   256-byte aligned, zero-filled before first use; every call
+ *                   leaves its counters zero
+ */
+int krk_gemm_bf16_select(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                         void* y, int64_t ldy, int M, int N, int K, int k,
+                         int64_t* idx, void* vals,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* krk_gemm_bf16_select with an explicit configuration: a VALU plan of depth
+ * (unroll) 5 with M <= 4, or an MFMA_LDS plan with k_chunk 256 and n_tiles 2
+ * or 4; K unsplit. */
+int krk_gemm_bf16_select_config(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                void* y, int64_t ldy, int M, int N, int K, int k,
+                                int64_t* idx, void* vals, const krk_gemm_config* cfg,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of a selecting call (cfg may be NULL: the plan); 0 for an
+ * invalid shape, k or configuration. */
+size_t krk_gemm_select_workspace_bytes(int M, int N, int K, int k, const krk_gemm_config* cfg);
+
+/* The configuration krk_gemm_bf16_select uses for this shape. */
+int krk_gemm_select_plan(int M, int N, int K, krk_gemm_config* out);
+
+/*
  * krk_last_error — text of the last error raised on the calling thread by
  * any krk_* function ("" if none).  Stands in for the ValueError messages of
  * engine/kernels/gateup64.py:63-74 and engine/kernels/gemm.py:253-254.

@@ -18,6 +18,7 @@
 #include "krk_mfma.h"
 #include "krk_mfma_lds.h"
 #include "krk_norm.h"
+#include "krk_select.h"
 #include "krk_stream.h"
 #include "krk_valu.h"
 
@@ -39,7 +40,7 @@ constexpr int kCuCount = 256;  // MI355X: 8 XCDs x 32 CUs
 // LDS per workgroup this build plans for (the portable 64 KB), and what the
 // kernels' static __shared__ variables take beside the dynamic reduction area.
 constexpr size_t kLdsBudget = 65536;
-constexpr size_t kLdsReserve = 256;
+constexpr size_t kLdsReserve = 1024;
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -431,20 +432,21 @@ int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int NT, int PF, int KC, bool SILU>
-int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream) {
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false>
+int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::SelectArgs sa = {}) {
     if constexpr ((PF == 3 && !mfma_lds_pf3(MT, NT)) || !krk::mfma_lds_kc_ok(MT, NT, KC)) {
         return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS unroll=%d k_chunk=%d with %d x %d tiles", PF, KC, MT, NT);
     } else {
-        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU>);
-        const size_t shm = krk::mfma_lds_bytes(MT, NT, KC);
+        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU, SEL>);
+        const size_t shm = krk::mfma_lds_bytes(MT, NT, KC, SEL);
         // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once
         // per instantiation (a function attribute, not a stream operation).
         static const hipError_t attr =
             shm > 65536 ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) : hipSuccess;
         if (attr != hipSuccess) return hip_status(attr, "mfma_lds_kernel LDS attribute");
         void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
-                        (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr};
+                        (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr,
+                        (void*)&sa};
         hipError_t e = hipLaunchKernel(fn, dim3(nblocks * a.splits), dim3(64 * krk::kLdsWaves), args, shm, stream);
         return hip_status(e, "mfma_lds_kernel launch");
     }
@@ -545,26 +547,27 @@ int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, 
     return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
 
-template <int MX, int R, int D, bool SILU, bool NORM = false>
-int launch_valu(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream, krk::NormArgs na = {}) {
+template <int MX, int R, int D, bool SILU, bool NORM = false, bool SEL = false>
+int launch_valu(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream, krk::NormArgs na = {},
+                krk::SelectArgs sa = {}) {
     const int nb = cdiv(a.K, krk::kValuBlock);
     int per = nb / a.splits, rem = nb % a.splits;
     // Whole 512-element blocks and whole D-block chunks in every split: the
     // kernel variant without clamps or masks.
     const bool exact = a.K % krk::kValuBlock == 0 && rem == 0 && per % D == 0;
-    const void* fn = exact ? reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM>)
-                           : reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM>);
+    const void* fn = exact ? reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM, SEL>)
+                           : reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM, SEL>);
     const size_t shm = NORM ? krk::valu_norm_lds_bytes(MX, nb) : krk::valu_lds_bytes(MX, cdiv(nb, a.splits));
     if (NORM || MX >= krk::kValuLdsMinRows) {
         static const hipError_t attr[2] = {
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM, SEL>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax),
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM, SEL>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax)};
         if (attr[exact] != hipSuccess) return hip_status(attr[exact], "valu_gemm_kernel LDS attribute");
     }
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy, (void*)&a.M,
-                    (void*)&a.N, (void*)&a.K,   (void*)&per, (void*)&rem, (void*)&a.part, (void*)&a.ctr, (void*)&na};
+                    (void*)&a.N, (void*)&a.K,   (void*)&per, (void*)&rem, (void*)&a.part, (void*)&a.ctr, (void*)&na, (void*)&sa};
     hipError_t e = hipLaunchKernel(fn, dim3(nblocks, a.splits), dim3(64 * waves), args, shm, stream);
     return hip_status(e, "valu_gemm_kernel launch");
 }
@@ -801,6 +804,136 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     return KRK_OK;
 }
 
+// ----------------------------------------------------------------- token selection
+// The lm_head projection with per-row argmax / top-k fused (krk_select.h).
+// Plans: the VALU kernel where the table picks it (M <= 4 at the depth that
+// covers K = 2560 in one pass), otherwise the LDS-staged MFMA kernel with
+// 256-k stages; K is never split.
+constexpr int kSelValuMaxRows = 4;
+
+template <int MX>
+int dispatch_valu_sel(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s, const krk::SelectArgs& sa) {
+    if (c.n_tiles == 1) return launch_valu<MX, 1, kValuNormDepth, false, false, true>(a, nblocks, c.waves, s, {}, sa);
+    if (c.n_tiles == 2) return launch_valu<MX, 2, kValuNormDepth, false, false, true>(a, nblocks, c.waves, s, {}, sa);
+    if (c.n_tiles == 4) return launch_valu<MX, 4, kValuNormDepth, false, false, true>(a, nblocks, c.waves, s, {}, sa);
+    return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles=%d", c.n_tiles);
+}
+
+template <int MT>
+int dispatch_mfma_lds_sel(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s, const krk::SelectArgs& sa) {
+    const bool pf3 = c.unroll == 3;
+    if (c.n_tiles == 2) return pf3 ? launch_mfma_lds<MT, 2, 3, 256, false, true>(a, nblocks, s, sa)
+                                   : launch_mfma_lds<MT, 2, 2, 256, false, true>(a, nblocks, s, sa);
+    if (c.n_tiles == 4) return pf3 ? launch_mfma_lds<MT, 4, 3, 256, false, true>(a, nblocks, s, sa)
+                                   : launch_mfma_lds<MT, 4, 2, 256, false, true>(a, nblocks, s, sa);
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS n_tiles=%d", c.n_tiles);
+}
+
+bool select_supported(const krk_gemm_config& c, int Mc) {
+    if (c.splits != 1) return false;
+    if (c.kernel == KRK_KERNEL_VALU) return c.m_tiles <= kSelValuMaxRows && c.unroll == kValuNormDepth;
+    if (c.kernel == KRK_KERNEL_MFMA_LDS)
+        return c.k_chunk == 256 && (c.n_tiles == 2 || c.n_tiles == 4) && c.m_tiles >= cdiv(Mc, 16) &&
+               (c.unroll == 2 || (c.unroll == 3 && mfma_lds_pf3(c.m_tiles, c.n_tiles)));
+    return false;
+}
+
+int select_config(int M, int N, int K, const krk_gemm_config* cfg, krk_gemm_config* out) {
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    krk_gemm_config c;
+    int rc = resolve_config(M, N, K, KRK_EPILOGUE_NONE, cfg, &c);
+    if (rc) return rc;
+    if (!select_supported(c, Mc)) {
+        if (cfg) return fail(KRK_ERR_UNSUPPORTED, "token selection runs on VALU plans of depth %d with M <= %d or on "
+                             "MFMA_LDS plans with k_chunk 256, n_tiles 2 or 4, unsplit K", kValuNormDepth, kSelValuMaxRows);
+        c = krk_gemm_config{KRK_KERNEL_MFMA_LDS, cdiv(Mc, 16), N >= 65536 && Mc > 8 ? 4 : 2, 2, krk::kLdsWaves, 1, 256};
+    }
+    *out = c;
+    return KRK_OK;
+}
+
+size_t select_workspace(int M, int N, int K, int k, const krk_gemm_config& c) {
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    const Geometry g = geometry(Mc, N, KRK_EPILOGUE_NONE, c);
+    return krk::select_layout(g.nblocks, Mc, k).total;
+}
+
+int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy, int M, int N, int K,
+                int k, int64_t* idx, void* vals, const krk_gemm_config* cfg, void* workspace, size_t workspace_bytes,
+                void* stream) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, KRK_EPILOGUE_NONE);
+    if (rc) return rc;
+    if (k < 1 || k > krk::kSelMaxK || k > N) return fail(KRK_ERR_INVALID, "k=%d must be in 1..min(%d, N)", k, krk::kSelMaxK);
+    if (!x || !w || !idx) return fail(KRK_ERR_INVALID, "null operand pointer (x=%p w=%p idx=%p)", x, w, idx);
+    if (ldx < K || ldw < K) return fail(KRK_ERR_INVALID, "ldx=%lld / ldw=%lld must be >= K=%d", (long long)ldx, (long long)ldw, K);
+    if ((ldx % 8) || (ldw % 8)) return fail(KRK_ERR_ALIGN, "ldx=%lld and ldw=%lld must be multiples of 8 elements", (long long)ldx, (long long)ldw);
+    if (((uintptr_t)x % 16) || ((uintptr_t)w % 16)) return fail(KRK_ERR_ALIGN, "x=%p and w=%p must be 16-byte aligned", x, w);
+    if ((uintptr_t)idx % 8 || (uintptr_t)vals % 2 || (uintptr_t)y % 2) return fail(KRK_ERR_ALIGN, "idx, vals or y misaligned");
+    if (y && ldy < N) return fail(KRK_ERR_INVALID, "ldy=%lld must be >= N=%d", (long long)ldy, N);
+    krk_gemm_config c;
+    if ((rc = select_config(M, N, K, cfg, &c))) return rc;
+
+    const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((uint64_t)(M - 1) * ldx + K) * 2;
+    const uintptr_t w0 = (uintptr_t)w, w1 = w0 + ((uint64_t)(N - 1) * ldw + K) * 2;
+    const uintptr_t i0 = (uintptr_t)idx, i1 = i0 + (uint64_t)M * k * 8;
+    const uintptr_t v0 = (uintptr_t)vals, v1 = vals ? v0 + (uint64_t)M * k * 2 : v0;
+    const uintptr_t y0 = (uintptr_t)y, y1 = y ? y0 + ((uint64_t)(M - 1) * ldy + N) * 2 : y0;
+    const uintptr_t s0 = (uintptr_t)workspace;
+    const size_t need = select_workspace(M, N, K, k, c);
+    const uintptr_t s1 = s0 + need;
+    struct Span { uintptr_t a, b; } outs[] = {{i0, i1}, {v0, v1}, {y0, y1}, {s0, s1}};
+    for (int p = 0; p < 4; ++p) {
+        if (outs[p].a == outs[p].b) continue;
+        if (overlaps(outs[p].a, outs[p].b, x0, x1) || overlaps(outs[p].a, outs[p].b, w0, w1))
+            return fail(KRK_ERR_ALIAS, "outputs and workspace may not share memory with x or W");
+        for (int q = p + 1; q < 4; ++q)
+            if (outs[q].a != outs[q].b && overlaps(outs[p].a, outs[p].b, outs[q].a, outs[q].b))
+                return fail(KRK_ERR_ALIAS, "idx, vals, y and the workspace may not overlap");
+    }
+    if (!workspace) return fail(KRK_ERR_WORKSPACE, "token selection needs a %zu-byte workspace, got none", need);
+    if (workspace_bytes < need) return fail(KRK_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, need);
+    if ((uintptr_t)workspace % 256) return fail(KRK_ERR_ALIGN, "workspace=%p must be 256-byte aligned", workspace);
+
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int m0 = 0; m0 < M; m0 += kMaxRowsPerLaunch) {
+        LaunchArgs a;
+        a.x = static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx;
+        a.ldx = ldx;
+        a.w = static_cast<const uint16_t*>(w);
+        a.ldw = ldw;
+        a.y = y ? static_cast<uint16_t*>(y) + (int64_t)m0 * ldy : nullptr;
+        a.ldy = ldy;
+        a.M = (M - m0) < kMaxRowsPerLaunch ? (M - m0) : kMaxRowsPerLaunch;
+        a.N = N;
+        a.K = K;
+        a.splits = 1;
+        a.part = nullptr;
+        a.ctr = nullptr;
+        const Geometry g = geometry(a.M, N, KRK_EPILOGUE_NONE, c);
+        krk::SelectArgs sa{static_cast<unsigned char*>(workspace), idx + (int64_t)m0 * k,
+                           vals ? static_cast<uint16_t*>(vals) + (int64_t)m0 * k : nullptr, k};
+        if (c.kernel == KRK_KERNEL_VALU) {
+            switch (c.m_tiles) {
+                case 1: rc = dispatch_valu_sel<1>(a, c, g.nblocks, st, sa); break;
+                case 2: rc = dispatch_valu_sel<2>(a, c, g.nblocks, st, sa); break;
+                case 4: rc = dispatch_valu_sel<4>(a, c, g.nblocks, st, sa); break;
+                default: rc = fail(KRK_ERR_UNSUPPORTED, "VALU x rows=%d", c.m_tiles);
+            }
+        } else {
+            switch (c.m_tiles) {
+                case 1: rc = dispatch_mfma_lds_sel<1>(a, c, g.nblocks, st, sa); break;
+                case 2: rc = dispatch_mfma_lds_sel<2>(a, c, g.nblocks, st, sa); break;
+                case 3: rc = dispatch_mfma_lds_sel<3>(a, c, g.nblocks, st, sa); break;
+                case 4: rc = dispatch_mfma_lds_sel<4>(a, c, g.nblocks, st, sa); break;
+                default: rc = fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
+            }
+        }
+        if (rc) return rc;
+    }
+    return KRK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -879,6 +1012,33 @@ int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd
     hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&krk::add_rmsnorm_kernel), dim3(M),
                                    dim3(krk::kNormThreads), args, 0, static_cast<hipStream_t>(stream));
     return hip_status(e, "add_rmsnorm_kernel launch");
+}
+
+int krk_gemm_bf16_select(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                         int M, int N, int K, int k, int64_t* idx, void* vals,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    return select_impl(x, ldx, w, ldw, y, ldy, M, N, K, k, idx, vals, nullptr, workspace, workspace_bytes, stream);
+}
+
+int krk_gemm_bf16_select_config(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                                int M, int N, int K, int k, int64_t* idx, void* vals, const krk_gemm_config* cfg,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    return select_impl(x, ldx, w, ldw, y, ldy, M, N, K, k, idx, vals, cfg, workspace, workspace_bytes, stream);
+}
+
+size_t krk_gemm_select_workspace_bytes(int M, int N, int K, int k, const krk_gemm_config* cfg) {
+    if (check_shape(M, N, K, KRK_EPILOGUE_NONE) || k < 1 || k > krk::kSelMaxK || k > N) return 0;
+    krk_gemm_config c;
+    if (select_config(M, N, K, cfg, &c)) return 0;
+    return select_workspace(M, N, K, k, c);
+}
+
+int krk_gemm_select_plan(int M, int N, int K, krk_gemm_config* out) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, KRK_EPILOGUE_NONE);
+    if (rc) return rc;
+    if (!out) return fail(KRK_ERR_INVALID, "null output config");
+    return select_config(M, N, K, nullptr, out);
 }
 
 size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue) {

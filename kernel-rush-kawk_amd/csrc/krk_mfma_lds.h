@@ -36,6 +36,7 @@
 #pragma once
 
 #include "krk_epilogue.h"
+#include "krk_select.h"
 
 namespace krk {
 
@@ -47,20 +48,24 @@ constexpr int kLdsWaves = 8;
 __host__ __device__ constexpr bool mfma_lds_kc_ok(int MT, int NT, int KC) {
     return KC == 256 || (KC == 512 && MT + NT <= 4);
 }
-// Dynamic LDS bytes: two tiles, which the final reduction reuses.
-__host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC) {
+// Dynamic LDS bytes: two tiles, which the final reduction reuses (with token
+// selection, followed by the bf16 outputs [16·MT][16·NT]).
+__host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool sel = false) {
     const size_t tile = (size_t)2 * 16 * (NT + MT) * 2 * KC;
-    const size_t red = (size_t)kLdsWaves * MT * NT * 64 * 16;
+    const size_t red = (size_t)kLdsWaves * MT * NT * 64 * 16 + (sel ? (size_t)16 * MT * 16 * NT * 2 : 0);
     return tile > red ? tile : red;
 }
 
-template <int MT, int NT, int PF, int KC, bool SILU>
+// SEL: token selection (krk_select.h) instead of, or besides, storing y (y may
+// be null); K unsplit.
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false>
 __global__ void __launch_bounds__(64 * kLdsWaves)
 mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const uint16_t* __restrict__ w, int64_t ldw,
                 uint16_t* __restrict__ y, int64_t ldy,
                 int M, int N, int K, int splits,
-                float* __restrict__ part, uint32_t* __restrict__ ctr) {
+                float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa) {
+    static_assert(!(SEL && SILU), "selection reads plain logits");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     static_assert(!SILU || (NT % 2 == 0), "SILU pairs gate and up tiles");
     static_assert(PF >= 2, "at least two stages in flight");
@@ -197,6 +202,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     __syncthreads();
 
     OutStage<SILU> o{y, ldy, part, M, N, Nout, splits, s};
+    uint16_t* const selv = reinterpret_cast<uint16_t*>(smem + (size_t)WV * MT * NT * 64 * 16);  // [16·MT][16·NT]
     const int items = MT * NH * 64;
     for (int v = threadIdx.x; v < items; v += blockDim.x) {
         const int ln = v & 63;
@@ -211,13 +217,27 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         }
         const int c = c0 + 16 * tl + (ln & 15);
         const int mb = 16 * i + 4 * (ln >> 4);
-        if (c < Nout) {
+        if constexpr (SEL) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) selv[(mb + e) * (16 * NT) + 16 * tl + (ln & 15)] = (uint16_t)f32_to_bf16(gsum[e]);
+            if (y && c < Nout) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (mb + e < M) o.put(mb + e, c, gsum[e], usum[e]);
+            }
+        } else if (c < Nout) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (mb + e < M) o.put(mb + e, c, gsum[e], usum[e]);
         }
     }
-    if (splits > 1) splitk_finish<SILU>(o, ctr, blk, c0, 16 * NH);
+    if constexpr (SEL) {
+        __syncthreads();
+        const int n = 16 * NT < Nout - c0 ? 16 * NT : Nout - c0;
+        select_local(sa, selv, 16 * NT, n, c0, M, blockIdx.x, gridDim.x);
+    } else if (splits > 1) {
+        splitk_finish<SILU>(o, ctr, blk, c0, 16 * NH);
+    }
 }
 
 }  // namespace krk

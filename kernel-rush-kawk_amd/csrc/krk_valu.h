@@ -29,6 +29,7 @@
 
 #include "krk_epilogue.h"
 #include "krk_norm.h"
+#include "krk_select.h"
 #include "krk_sync.h"
 
 namespace krk {
@@ -137,12 +138,15 @@ constexpr int log2_exact() {
 // covers waves * R (SILU: waves * R/2) consecutive output channels.  Split s
 // owns K blocks [s*per + min(s, rem), ...) where per = nb / splits and
 // rem = nb % splits (nb = ceil(K / 512)), so no division runs on the device.
-template <int MX, int R, int D, bool SILU, bool EXACT, bool NORM = false>
+// SEL: token selection (krk_select.h) instead of, or besides, storing y (y may
+// be null); K unsplit.
+template <int MX, int R, int D, bool SILU, bool EXACT, bool NORM = false, bool SEL = false>
 __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w, int64_t ldw,
     uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int per, int rem,
-    float* __restrict__ part, uint32_t* __restrict__ ctr, NormArgs na) {
+    float* __restrict__ part, uint32_t* __restrict__ ctr, NormArgs na, SelectArgs sa) {
     static_assert(!SILU || R % 2 == 0, "SILU pairs gate and up rows");
+    static_assert(!(SEL && SILU), "selection reads plain logits");
     constexpr bool XLDS = MX >= kValuLdsMinRows || NORM;
     static_assert(((XLDS ? 0 : MX) + R) * D < 64, "vmcnt counts at most 63 loads");
     constexpr int RO = SILU ? R / 2 : R;  // output channels per wave
@@ -373,8 +377,16 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     if constexpr (SILU) u = __shfl_down(acc[0], RO * G);
     const OutStage<SILU> o{y, ldy, part, M, N, Nout, splits, s};
     const int c = c0 + wave * RO + r;
-    if ((lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
-    if (splits > 1) splitk_finish<SILU, 4, 1>(o, ctr, blk, c0, cb);
+    if constexpr (SEL) {
+        __shared__ uint16_t selv[MX * kValuMaxWaves * R];  // [m][channel of the workgroup]
+        if ((lane & (G - 1)) == 0 && r < RO) selv[m * cb + wave * RO + r] = (uint16_t)f32_to_bf16(acc[0]);
+        if (y && (lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
+        __syncthreads();
+        select_local(sa, selv, cb, cb < Nout - c0 ? cb : Nout - c0, c0, M, blk, gridDim.x);
+    } else {
+        if ((lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
+        if (splits > 1) splitk_finish<SILU, 4, 1>(o, ctr, blk, c0, cb);
+    }
 }
 
 }  // namespace krk

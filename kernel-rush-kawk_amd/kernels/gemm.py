@@ -14,6 +14,8 @@ Python surface of libkrk_gemm.so, shaped like the reference's
 * ``norm=(y, w_norm, xout, eps)`` on every call, :func:`pick_normed` and
   :func:`add_rms_norm` — the residual-add + RMSNorm prologue (reference
   engine/kernels/gemm.py:21-51, 501-560 and engine/kernels/add_rmsnorm.py);
+* :class:`SkinnySelect` — the lm_head projection with per-row argmax / top-k
+  fused (reference consumers engine/engine.py:196, engine/recycle.py:170);
 * :func:`_time` — CUDA/HIP-graph replay timer (engine/kernels/gemm.py:378-414).
 
 All compute runs in the HIP kernels of libkrk_gemm.so; nothing here falls
@@ -32,8 +34,8 @@ from . import _lib
 from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
-    "SkinnyMatmul", "SkinnyGateUp", "Gemv", "pick_matmul", "pick_gateup", "pick_normed", "add_rms_norm", "plan",
-    "gemm_into", "normed_fused", "_time",
+    "SkinnyMatmul", "SkinnyGateUp", "Gemv", "SkinnySelect", "pick_matmul", "pick_gateup", "pick_normed",
+    "add_rms_norm", "plan", "select_plan", "gemm_into", "normed_fused", "_time",
 ]
 
 
@@ -389,3 +391,74 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
         fused = "fused" if normed_fused(M, N, K, mm.epilogue) else "prologue kernel"
         log(f"normed {kind} M={M} N={N} K={K}: krk{mm.resolved_config} ({fused}) {ms * 1000:.1f}us")
     return fn
+
+
+def select_plan(M: int, N: int, K: int) -> dict:
+    """The configuration a selecting lm_head call uses for this shape."""
+    cfg = GemmConfig()
+    _lib.check(_lib.load().krk_gemm_select_plan(M, N, K, ctypes.byref(cfg)))
+    return cfg.as_dict()
+
+
+class SkinnySelect:
+    """The lm_head projection with token selection fused: ``f(a, w)`` returns
+    the ``[M, k]`` int64 indices of each row's k largest bf16 logits of
+    ``a @ w.T`` (largest first, equal values at the lower index first, NaN
+    above everything), without writing the logits unless ``logits`` is given.
+    ``k = 1`` is ``(a @ w.T).argmax(dim=-1, keepdim=True)`` (engine/engine.py:196),
+    ``k = 8`` the ``torch.topk(logits, 8).indices`` of engine/recycle.py:170.
+    The workspace belongs to the object (zero-filled once; calls leave it so)."""
+
+    def __init__(self, M: int, N: int, K: int, device, k: int = 1, config: dict | None = None):
+        if M < 1 or N < 1 or K < 8 or K % 8:
+            raise ValueError(f"unsupported shape M={M} N={N} K={K} (need K >= 8, K % 8 == 0)")
+        self.M, self.N, self.K, self.k = M, N, K, k
+        self.device = torch.device(device)
+        self.config = dict(config) if config else None
+        cfg = GemmConfig.from_dict(config) if config else None
+        nbytes = int(_lib.load().krk_gemm_select_workspace_bytes(M, N, K, k, ctypes.byref(cfg) if cfg else None))
+        if nbytes == 0:
+            raise ValueError(f"no token-selection plan for M={M} N={N} K={K} k={k} config={config}: "
+                             f"{_lib.last_error() or 'k must be 1..8 and <= N'}")
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+
+    @property
+    def resolved_config(self) -> dict:
+        return dict(self.config) if self.config else select_plan(self.M, self.N, self.K)
+
+    def run(self, a: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, logits: torch.Tensor | None = None,
+            values: torch.Tensor | None = None) -> torch.Tensor:
+        """Allocation-free form: indices into ``idx`` ([M, k] int64), optionally
+        the logits into ``logits`` ([M, N] bf16) and the selected values into
+        ``values`` ([M, k] bf16)."""
+        M, K, N, k = self.M, self.K, self.N, self.k
+        _check_operand("a", a, M, K)
+        _check_operand("w", w, N, K)
+        if logits is not None:
+            _check_operand("logits", logits, M, N)
+        if idx.dtype != torch.int64 or tuple(idx.shape) != (M, k) or not idx.is_contiguous():
+            raise ValueError(f"idx must be a contiguous int64 tensor of shape ({M}, {k})")
+        if values is not None and (values.dtype != torch.bfloat16 or tuple(values.shape) != (M, k)
+                                   or not values.is_contiguous()):
+            raise ValueError(f"values must be a contiguous bf16 tensor of shape ({M}, {k})")
+        for name, t in (("a", a), ("w", w), ("idx", idx), ("logits", logits), ("values", values)):
+            if t is not None and t.device != self.device:
+                raise ValueError(f"{name} must be on {self.device}, got {t.device}")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        lib = _lib.load()
+        y_ptr, ldy = (logits.data_ptr(), logits.stride(0)) if logits is not None else (0, N)
+        v_ptr = values.data_ptr() if values is not None else 0
+        head = (a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), y_ptr, ldy, M, N, K, k, idx.data_ptr(), v_ptr)
+        ws = (self.workspace.data_ptr(), self.workspace.numel())
+        with torch.cuda.device(self.device):
+            if self.config is None:
+                rc = lib.krk_gemm_bf16_select(*head, *ws, stream)
+            else:
+                cfg = GemmConfig.from_dict(self.config)
+                rc = lib.krk_gemm_bf16_select_config(*head, ctypes.byref(cfg), *ws, stream)
+        _lib.check(rc)
+        return idx
+
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
+        idx = torch.empty((self.M, self.k), dtype=torch.int64, device=a.device)
+        return self.run(a, w, idx, logits)

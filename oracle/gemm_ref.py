@@ -104,6 +104,26 @@ def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     return torch.argmax(logits.detach().to("cpu").float(), dim=-1)
 
 
+def topk_rows(logits: torch.Tensor, k: int):
+    """Per-row indices and values of the k largest bf16 logits: larger value
+    first, equal values at the lower index first, every NaN above +inf, -0
+    equal to +0.  k = 1 is torch.argmax's choice (engine/engine.py:196, lowest
+    index on ties per OPTIMIZATION_GUIDE.md:213); for distinct values it is
+    torch.topk's (engine/recycle.py:170), whose order among equal values is
+    unspecified."""
+    b = to_bits(logits.detach().to("cpu", torch.bfloat16)).astype(np.uint32)
+    nan = (b & 0x7FFF) > 0x7F80
+    b = np.where(b == 0x8000, 0, b)
+    o = np.where(b & 0x8000, (~b) & 0xFFFF, b | 0x8000)
+    o = np.where(nan, 0xFFFF, o).astype(np.int64)
+    M, N = o.shape
+    n_idx = np.arange(N, dtype=np.int64)
+    key = (o << 32) - n_idx[None, :]          # larger value, then lower index, is larger
+    order = np.argsort(-key, axis=1, kind="stable")[:, :k]
+    vals = np.take_along_axis(to_bits(logits.detach().to("cpu", torch.bfloat16)), order, axis=1)
+    return torch.from_numpy(order), from_bits(vals)
+
+
 # --------------------------------------------------------------------------
 # bf16 bit helpers (numpy has no bf16 dtype; bf16 travels as uint16 bits)
 # --------------------------------------------------------------------------

@@ -303,3 +303,57 @@ def test_add_rms_norm_argument_errors(lib, kw, code):
     rc = lib.krk_add_rms_norm_bf16(a["x"], a["ldx"], a["d"], a["ldd"], a["g"], a["eps"], a["xo"], a["ldxo"],
                                    a["out"], a["ldo"], a["M"], a["K"], None)
     assert rc == code, _lib.last_error()
+
+
+# ------------------------------------------------------------------ fused token selection
+
+# The lm_head weight spans 778 MB: select calls keep everything else far from it.
+W_LM, IDX, WS_SEL, Y_SEL = 0x100000000, 0x300000000, 0x400000000, 0x500000000
+
+
+def call_select(lib, x=X, ldx=2560, w=W_LM, ldw=2560, y=0, ldy=151936, M=1, N=151936, K=2560, k=1, idx=IDX, vals=0,
+                ws=WS_SEL, wsb=1 << 30):
+    return lib.krk_gemm_bf16_select(x, ldx, w, ldw, y, ldy, M, N, K, k, idx, vals, ws, wsb, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(k=0), _lib.KRK_ERR_INVALID, "k="),
+    (dict(k=9), _lib.KRK_ERR_INVALID, "k="),
+    (dict(k=8, N=5, ldy=5), _lib.KRK_ERR_INVALID, "k="),
+    (dict(idx=0), _lib.KRK_ERR_INVALID, "null operand"),
+    (dict(idx=IDX + 4), _lib.KRK_ERR_ALIGN, "misaligned"),
+    (dict(y=Y_SEL, ldy=100), _lib.KRK_ERR_INVALID, "ldy"),
+    (dict(idx=X + 64), _lib.KRK_ERR_ALIAS, "may not share"),
+    (dict(idx=W_LM + 4096), _lib.KRK_ERR_ALIAS, "may not share"),
+    (dict(ws=IDX), _lib.KRK_ERR_ALIAS, "may not overlap"),
+    (dict(y=Y_SEL, vals=Y_SEL + 64), _lib.KRK_ERR_ALIAS, "may not overlap"),
+    (dict(ws=0), _lib.KRK_ERR_WORKSPACE, "workspace"),
+    (dict(wsb=64), _lib.KRK_ERR_WORKSPACE, "workspace"),
+    (dict(ws=WS_SEL + 16), _lib.KRK_ERR_ALIGN, "256-byte"),
+])
+def test_select_argument_errors(lib, kw, code, msg):
+    assert call_select(lib, **kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_select_plan_and_workspace(lib):
+    """VALU plans up to M = 4, the LDS-staged MFMA kernel with 256-k stages
+    beyond (never the persistent stream kernel); the workspace holds one
+    candidate list per workgroup and per group of 256."""
+    for M, kernel in [(1, _lib.KERNEL_VALU), (4, _lib.KERNEL_VALU), (5, _lib.KERNEL_MFMA_LDS),
+                      (32, _lib.KERNEL_MFMA_LDS), (64, _lib.KERNEL_MFMA_LDS), (100, _lib.KERNEL_MFMA_LDS)]:
+        cfg = GemmConfig()
+        assert lib.krk_gemm_select_plan(M, 151936, 2560, ctypes.byref(cfg)) == 0
+        c = cfg.as_dict()
+        assert c["kernel"] == kernel and c["splits"] == 1, (M, c)
+        if kernel == _lib.KERNEL_MFMA_LDS:
+            assert c["k_chunk"] == 256
+        Mc = min(M, 64)
+        G = -(-151936 // _channels_per_block(c, NONE))
+        ng = -(-G // 256)
+        al = lambda v: -(-v // 256) * 256
+        for k in (1, 8):
+            want = al(ng * 4) + 256 + al(G * Mc * k * 8) + al(ng * Mc * k * 8)
+            assert lib.krk_gemm_select_workspace_bytes(M, 151936, 2560, k, None) == want
+    bad = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_STREAM))
+    assert lib.krk_gemm_select_workspace_bytes(32, 151936, 2560, 1, ctypes.byref(bad)) == 0

@@ -645,3 +645,128 @@ def test_pick_normed_returns_validated_callable(device):
     wgu = R.randn_bf16((2 * 9728, K), 9802, 0.02).to(device)
     g = G.pick_normed("gateup", x, y, wn, wgu, EPS)
     assert g(x, y, wn, xo, wgu).shape == (M, 9728)
+
+
+# ------------------------------------------------------------------ fused token selection (lm_head argmax / top-k)
+
+def krk_select(x, w, k, config=None, logits=True, device="cuda:0", wd=None):
+    """Selecting HIP call on CPU inputs; returns (idx, vals, logits or None) on the CPU."""
+    M, K = x.shape
+    N = w.shape[0]
+    op = G.SkinnySelect(M, N, K, device, k, config)
+    xd = x.to(device)
+    wd = w.to(device) if wd is None else wd
+    lg = torch.empty((M, N), dtype=torch.bfloat16, device=device) if logits else None
+    vals = torch.empty((M, k), dtype=torch.bfloat16, device=device)
+    idx = torch.empty((M, k), dtype=torch.int64, device=device)
+    op.run(xd, wd, idx, lg, vals)
+    torch.cuda.synchronize()
+    return idx.cpu(), vals.cpu(), (lg.cpu() if logits else None)
+
+
+def _check_selection(idx, vals, logits, k, what):
+    """Bit-exact: the selection equals the oracle's top-k of the same logits."""
+    ref_idx, ref_vals = R.topk_rows(logits, k)
+    if not torch.equal(idx, ref_idx):
+        rows = (idx != ref_idx).any(dim=1).nonzero().flatten().tolist()
+        pytest.fail(f"{what}: selection differs on rows {rows[:5]}: got {idx[rows[0]].tolist()} "
+                    f"want {ref_idx[rows[0]].tolist()}")
+    # A NaN is reported as the canonical quiet NaN; every other value bit for bit.
+    gb, rb = R.to_bits(vals), R.to_bits(ref_vals)
+    gnan, rnan = (gb & 0x7FFF) > 0x7F80, (rb & 0x7FFF) > 0x7F80
+    assert np.array_equal(gnan, rnan) and np.array_equal(gb[~gnan], rb[~rnan]), f"{what}: selected values differ"
+
+
+@pytest.fixture(scope="module")
+def lm_head_dev(lm_head):
+    return lm_head.to("cuda:0")
+
+
+@pytest.mark.parametrize("k", [1, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 16, 17, 32, 64, 100])
+def test_select_lm_head(device, lm_head, lm_head_dev, M, k):
+    x = R.randn_bf16((M, R.HIDDEN), R.seed_for(5, M, "x") + 7)
+    say("select lm_head", M, k, G.select_plan(M, R.VOCAB, R.HIDDEN))
+    idx, vals, logits = krk_select(x, lm_head, k, wd=lm_head_dev)
+    _check_selection(idx, vals, logits, k, f"select M={M} k={k}")
+    ref = R.linear_bf16(x, lm_head)
+    assert_parity(logits, ref, f"select logits M={M}")
+    if k == 1:
+        assert torch.equal(idx[:, 0], R.argmax_rows(ref)), f"select M={M}: argmax differs from the oracle's"
+    idx2, vals2, _ = krk_select(x, lm_head, k, logits=False, wd=lm_head_dev)
+    assert torch.equal(idx, idx2) and torch.equal(vals, vals2), "selection without logits differs"
+
+
+def _tie_weights(N, K, seed):
+    """W whose rows repeat: row 3·i + j = row 3·i for j < 3, so equal logits
+    sit at consecutive indices; one row pair is NaN-producing."""
+    base = R.randn_bf16((-(-N // 3), K), seed, 0.02)
+    w = base.repeat_interleave(3, dim=0)[:N].clone()
+    return w
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 2560), (3, 4099, 2560), (4, 300, 2560), (7, 1000, 512),
+                                   (33, 5000, 2560), (64, 257, 1024)])
+def test_select_ties_nan_and_configs(device, M, N, K):
+    """Equal logits (repeated W rows) rank the lower index first; a NaN logit
+    ranks above everything; every selection configuration agrees bit for bit."""
+    x = R.randn_bf16((M, K), 9900 + M)
+    w = _tie_weights(N, K, 9901 + N)
+    w[N // 2, 0] = float("nan")         # logits of row N//2 are NaN in every row m
+    cfgs = [None]
+    if M <= 4 and K == 2560:
+        cfgs += [dict(kernel=_lib.KERNEL_VALU, unroll=5, n_tiles=nt, waves=wv, splits=1)
+                 for nt in (1, 2, 4) for wv in (1, 4, 8)]
+    cfgs += [dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=nt, unroll=pf, k_chunk=256, splits=1)
+             for nt in (2, 4) for pf in (2, 3)]
+    base = None
+    for cfg in cfgs:
+        for k in (1, 8):
+            say("select ties", M, N, K, k, cfg)
+            try:
+                idx, vals, logits = krk_select(x, w, k, cfg)
+            except ValueError as e:  # a combination the library does not provide (e.g. unroll 3 on big tiles)
+                assert cfg is not None and "no token-selection plan" in str(e), e
+                continue
+            _check_selection(idx, vals, logits, k, f"select {cfg} k={k}")
+            assert (idx[:, 0] == N // 2).all(), "the NaN logit must rank first"
+            if k == 8:
+                base = idx if base is None else base
+                assert torch.equal(idx, base), f"select {cfg}: differs from the first configuration"
+
+
+def test_select_graph_replay(device, lm_head_dev):
+    """Selecting calls captured in a graph replay to the eager result several
+    times (their counters reset themselves), with eager work in between."""
+    cases = [(1, 1), (8, 8), (32, 1)]
+    ops, xs, eager, outs = [], [], [], []
+    for i, (M, k) in enumerate(cases):
+        op = G.SkinnySelect(M, R.VOCAB, R.HIDDEN, device, k)
+        x = R.randn_bf16((M, R.HIDDEN), 9950 + i).to(device)
+        ops.append(op)
+        xs.append(x)
+        eager.append(op(x, lm_head_dev).clone())
+        outs.append(torch.empty_like(eager[-1]))
+    torch.cuda.synchronize()
+    say("select graph", cases)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for op, x, o in zip(ops, xs, outs):
+            op.run(x, lm_head_dev, o)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for op, x, o in zip(ops, xs, outs):
+            op.run(x, lm_head_dev, o)
+    for rep in range(3):
+        for o in outs:
+            o.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for e, o in zip(eager, outs):
+            assert torch.equal(e, o), f"select replay {rep} differs from eager"
+        _ = ops[0](xs[0], lm_head_dev)
+        torch.cuda.synchronize()

@@ -282,3 +282,47 @@ def test_normed_linear_composes_prologue_and_projection():
     assert torch.equal(out, R.linear_bf16(R.add_rms_norm_bf16(x, y, wn, 1e-6)[1], w))
     xo2, out2 = R.normed_gateup_bf16(x, y, wn, 1e-6, R.randn_bf16((2 * N, K), 65, 0.02))
     assert torch.equal(xo, xo2) and out2.shape == (M, N)
+
+
+# ------------------------------------------------------------------ token selection
+
+def test_topk_rows_k1_is_torch_argmax_and_the_c_restatement():
+    logits = R.randn_bf16((6, 3000), 71)
+    logits[2, 17] = logits[2].max()        # a tie with an earlier maximum... or a new one
+    logits[3, :] = 1.0                     # all equal: index 0
+    logits[4, 5] = float("-0.0")
+    logits[4, :5] = 0.0                    # -0 ties +0 when 0 is the max
+    logits[4, 6:] = -1.0
+    idx, _ = R.topk_rows(logits, 1)
+    assert torch.equal(idx[:, 0], torch.argmax(logits.float(), dim=-1))
+    assert torch.equal(idx[:, 0], R.c_argmax_rows(logits))
+    assert idx[3, 0] == 0 and idx[4, 0] == 0
+
+
+def test_topk_rows_nan_is_the_largest_value():
+    logits = R.randn_bf16((2, 50), 72)
+    logits[0, 30] = float("nan")
+    logits[0, 40] = float("nan")
+    logits[1, 7] = float("inf")
+    idx, _ = R.topk_rows(logits, 2)
+    assert idx[0].tolist() == [30, 40]
+    assert idx[0, 0] == torch.argmax(logits.float(), dim=-1)[0]
+    assert idx[1, 0] == 7
+
+
+def test_topk_rows_matches_torch_topk_on_distinct_values():
+    g = torch.Generator().manual_seed(73)
+    for N in (8, 200, 256):
+        vals = torch.randperm(N, generator=g).float().sub_(N // 2)  # distinct integers in [-128, 128): exact in bf16
+        logits = vals.reshape(1, N).to(torch.bfloat16)
+        for k in (1, 3, 8):
+            idx, v = R.topk_rows(logits, k)
+            ref = torch.topk(logits.float(), k, dim=-1)
+            assert torch.equal(idx, ref.indices) and torch.equal(v.float(), ref.values)
+
+
+def test_topk_rows_equal_values_take_the_lower_index_first():
+    logits = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0, -5.0]], dtype=torch.bfloat16)
+    idx, v = R.topk_rows(logits, 5)
+    assert idx[0].tolist() == [1, 2, 4, 3, 0]
+    assert v[0].float().tolist() == [3.0, 3.0, 3.0, 2.0, 1.0]
