@@ -285,6 +285,35 @@ def main() -> int:
                     f"   prologue+gemm {row['prologue_kernel_plus_gemm_us']:8.2f} us"
                     + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
 
+    # ------------------------------------------------------------ token selection
+    # lm_head followed by the per-row argmax (k = 1) or top-8, no caller
+    # logits (argmax fused into the VALU / LDS-staged MFMA projections writes
+    # none; other plans write them to the workspace and select from there),
+    # against the plain projection followed by torch.argmax / torch.topk on
+    # its logits (what the reference runs).
+    select = []
+    if not args.no_table:
+        K, Nw, _ = SHAPES["lm_head"]
+        for Mt in (1, 8, 32, 64):
+            xt = randn_bf16(torch, (Mt, K), 95 + Mt, 1.0, dev)
+            plain = G.SkinnyMatmul(Mt, Nw, K, dev)
+            lg = torch.empty((Mt, Nw), dtype=torch.bfloat16, device=dev)
+            for k in (1, 8):
+                op = G.SkinnySelect(Mt, Nw, K, dev, k)
+                idx = torch.empty((Mt, k), dtype=torch.int64, device=dev)
+                n = 2 * len(lm)
+                f_ms, _ = graph_time_ms(torch, [(lambda w=lm[i % len(lm)]: op.run(xt, w, idx)) for i in range(n)])
+                if k == 1:
+                    sel = lambda: torch.argmax(lg, dim=-1)
+                else:
+                    sel = lambda: torch.topk(lg, k, dim=-1).indices
+                u_ms, _ = graph_time_ms(torch, [(lambda w=lm[i % len(lm)]: (plain.run(xt, w, lg), sel())) for i in range(n)])
+                row = {"M": Mt, "k": k, "us": round(f_ms * 1000, 2), "plain_gemm_plus_torch_select_us": round(u_ms * 1000, 2),
+                       "fused": op.fused, "config": op.resolved_config}
+                select.append(row)
+                log(f"select M={Mt:3d} k={k}  {'fused' if op.fused else 'logits'} {row['us']:8.2f} us   lm_head + torch "
+                    f"{'argmax' if k == 1 else 'topk'} {row['plain_gemm_plus_torch_select_us']:8.2f} us")
+
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -313,6 +342,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "per_gemm": table,
         "normed": normed,
+        "select": select,
     }
     print(json.dumps(result), flush=True)
     return 0

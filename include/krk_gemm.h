@@ -214,11 +214,15 @@ int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd
                           void* out, int64_t ldo, int M, int K, void* stream);
 
 /*
- * krk_gemm_bf16_select — the lm_head projection with token selection fused:
+ * krk_gemm_bf16_select — the lm_head projection followed by token selection:
  * idx[m][0..k) = indices of the k largest bf16 logits bf16(x[m]·W[n]ᵀ) of
  * row m, largest first, equal values at the lower index first (NaN above
- * +inf, -0 equal to +0), without a second launch and without writing the
- * logits unless y is given.
+ * +inf, -0 equal to +0).  For k = 1 behind a VALU or LDS-staged MFMA
+ * projection (krk_gemm_select_fused) the projection's epilogue reduces its
+ * outputs to one key per row and workgroup and the logits are not written
+ * unless y is given; otherwise the plain projection writes the logits (to y,
+ * or to the workspace) and a selection kernel reads them back.  Either way
+ * the call is two kernels on one stream.
  *
  * Replaces `logits.argmax(dim=-1)` (k = 1; engine/engine.py:196,
  * engine/model.py:365; lowest index on ties, OPTIMIZATION_GUIDE.md:213) and
@@ -228,7 +232,7 @@ int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd
  *   x, w, M, N, K   as krk_gemm_bf16 (plain epilogue)
  *   y               [M, N] bf16 logits, stride ldy >= N, or NULL to skip them
  *   k               1..8 (<= N)
- *   idx             [M, k] int64 output (-1 past N), 8-byte aligned
+ *   idx             [M, k] int64 output, 8-byte aligned
  *   vals            [M, k] bf16 values of the selected logits (a NaN as the
  *                   canonical quiet NaN 0x7fc0), or NULL
  *   workspace       krk_gemm_select_workspace_bytes(M, N, K, k, NULL) bytes,
@@ -240,9 +244,8 @@ int krk_gemm_bf16_select(const void* x, int64_t ldx, const void* w, int64_t ldw,
                          int64_t* idx, void* vals,
                          void* workspace, size_t workspace_bytes, void* stream);
 
-/* krk_gemm_bf16_select with an explicit configuration: a VALU plan of depth
- * (unroll) 5 with M <= 4, or an MFMA_LDS plan with k_chunk 256 and n_tiles 2
- * or 4; K unsplit. */
+/* krk_gemm_bf16_select with an explicit projection configuration (any
+ * configuration krk_gemm_bf16_config accepts for the plain epilogue). */
 int krk_gemm_bf16_select_config(const void* x, int64_t ldx, const void* w, int64_t ldw,
                                 void* y, int64_t ldy, int M, int N, int K, int k,
                                 int64_t* idx, void* vals, const krk_gemm_config* cfg,
@@ -252,8 +255,14 @@ int krk_gemm_bf16_select_config(const void* x, int64_t ldx, const void* w, int64
  * invalid shape, k or configuration. */
 size_t krk_gemm_select_workspace_bytes(int M, int N, int K, int k, const krk_gemm_config* cfg);
 
-/* The configuration krk_gemm_bf16_select uses for this shape. */
-int krk_gemm_select_plan(int M, int N, int K, krk_gemm_config* out);
+/* The projection configuration krk_gemm_bf16_select uses for this shape and k. */
+int krk_gemm_select_plan(int M, int N, int K, int k, krk_gemm_config* out);
+
+/* 1 if the selection is fused into the projection's epilogue (the logits are
+ * then written only when y is given), 0 if the projection writes the logits
+ * and a selection kernel reads them, negative on an invalid shape, k or
+ * configuration (cfg may be NULL: the plan). */
+int krk_gemm_select_fused(int M, int N, int K, int k, const krk_gemm_config* cfg);
 
 /*
  * krk_last_error — text of the last error raised on the calling thread by

@@ -805,10 +805,19 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
 }
 
 // ----------------------------------------------------------------- token selection
-// The lm_head projection with per-row argmax / top-k fused (krk_select.h).
-// Plans: the VALU kernel where the table picks it (M <= 4 at the depth that
-// covers K = 2560 in one pass), otherwise the LDS-staged MFMA kernel with
-// 256-k stages; K is never split.
+// The lm_head projection followed by per-row argmax / top-k (krk_select.h).
+// Two plans:
+//   * fused (argmax behind a VALU or LDS-staged MFMA projection with unsplit
+//     K): the projection's epilogue writes one key per row and workgroup and
+//     select_rows_kernel reduces those keys; the logits are written only when
+//     the caller asks for them;
+//   * unfused (top-k, and every other projection plan, e.g. the stream kernel
+//     the table picks at M >= 17): the plain projection writes the bf16
+//     logits (to y, or to the workspace when y is null) and
+//     select_rows_kernel reduces them.
+// A top-k in the epilogue was measured and rejected: its per-workgroup
+// cross-lane rounds added 15-60% to the short projection workgroups, more
+// than the logits' round trip through HBM costs.
 constexpr int kSelValuMaxRows = 4;
 
 template <int MX>
@@ -829,7 +838,17 @@ int dispatch_mfma_lds_sel(const LaunchArgs& a, const krk_gemm_config& c, int nbl
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS n_tiles=%d", c.n_tiles);
 }
 
-bool select_supported(const krk_gemm_config& c, int Mc) {
+int dispatch_plain(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t st) {
+    switch (c.kernel) {
+        case KRK_KERNEL_MFMA: return dispatch_mfma<false>(a, c, nblocks, st);
+        case KRK_KERNEL_MFMA_LDS: return dispatch_mfma_lds<false>(a, c, nblocks, st);
+        case KRK_KERNEL_STREAM: return dispatch_stream<false>(a, c, nblocks, st);
+        default: return dispatch_valu<false>(a, c, nblocks, st);
+    }
+}
+
+// Whether argmax runs fused behind this projection plan (rows per launch Mc).
+bool select_fusable(const krk_gemm_config& c, int Mc) {
     if (c.splits != 1) return false;
     if (c.kernel == KRK_KERNEL_VALU) return c.m_tiles <= kSelValuMaxRows && c.unroll == kValuNormDepth;
     if (c.kernel == KRK_KERNEL_MFMA_LDS)
@@ -838,24 +857,59 @@ bool select_supported(const krk_gemm_config& c, int Mc) {
     return false;
 }
 
-int select_config(int M, int N, int K, const krk_gemm_config* cfg, krk_gemm_config* out) {
-    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+struct SelectPlan {
     krk_gemm_config c;
-    int rc = resolve_config(M, N, K, KRK_EPILOGUE_NONE, cfg, &c);
+    bool fused;
+};
+
+int select_plan_for(int M, int N, int K, int k, const krk_gemm_config* cfg, SelectPlan* out) {
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    int rc = resolve_config(M, N, K, KRK_EPILOGUE_NONE, cfg, &out->c);
     if (rc) return rc;
-    if (!select_supported(c, Mc)) {
-        if (cfg) return fail(KRK_ERR_UNSUPPORTED, "token selection runs on VALU plans of depth %d with M <= %d or on "
-                             "MFMA_LDS plans with k_chunk 256, n_tiles 2 or 4, unsplit K", kValuNormDepth, kSelValuMaxRows);
-        c = krk_gemm_config{KRK_KERNEL_MFMA_LDS, cdiv(Mc, 16), N >= 65536 && Mc > 8 ? 4 : 2, 2, krk::kLdsWaves, 1, 256};
-    }
-    *out = c;
+    out->fused = k == 1 && select_fusable(out->c, Mc);
     return KRK_OK;
 }
 
-size_t select_workspace(int M, int N, int K, int k, const krk_gemm_config& c) {
+// Workspace of a selecting call, for one launch of Mc rows (launches of a
+// call run in order on one stream and reuse it):
+//   [row counters, 256 B][projection split-K area][keys [Mc, ldk] u64 (fused)
+//    or logits [Mc, ldl] bf16 (unfused; unused when the caller passes y)]
+//   [chunk lists [Mc, C, k]]
+struct SelectLayout {
+    size_t proj, src, lists, total;
+    int64_t ld;  // row stride of the source in elements
+    int n;       // source elements per row
+    int chunks;  // select_rows_kernel chunks per row
+};
+SelectLayout select_layout(int M, int N, int k, const SelectPlan& p) {
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
-    const Geometry g = geometry(Mc, N, KRK_EPILOGUE_NONE, c);
-    return krk::select_layout(g.nblocks, Mc, k).total;
+    SelectLayout l;
+    l.proj = 256;
+    size_t at = align_up(l.proj + workspace_for(Mc, N, KRK_EPILOGUE_NONE, p.c), 256);
+    l.src = at;
+    if (p.fused) {
+        l.n = geometry(Mc, N, KRK_EPILOGUE_NONE, p.c).nblocks;
+        l.ld = align_up((size_t)l.n, 2);
+        at += align_up((size_t)Mc * l.ld * sizeof(uint64_t), 256);
+        l.chunks = cdiv(l.n, krk::kSelChunkKeys);
+    } else {
+        l.n = N;
+        l.ld = align_up((size_t)N, 8);
+        at += align_up((size_t)Mc * l.ld * sizeof(uint16_t), 256);
+        l.chunks = cdiv(N, krk::kSelChunkVals);
+    }
+    l.lists = at;
+    at += align_up((size_t)Mc * l.chunks * k * sizeof(uint64_t), 256);
+    l.total = at;
+    return l;
+}
+
+template <int KM, bool KEYS>
+int launch_select_rows(const krk::RowSelectArgs& ra, int chunks, int rows, hipStream_t st) {
+    void* args[] = {(void*)&ra};
+    hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&krk::select_rows_kernel<KM, KEYS>), dim3(chunks, rows),
+                                   dim3(krk::kSelThreads), args, 0, st);
+    return hip_status(e, "select_rows_kernel launch");
 }
 
 int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy, int M, int N, int K,
@@ -871,8 +925,9 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
     if (((uintptr_t)x % 16) || ((uintptr_t)w % 16)) return fail(KRK_ERR_ALIGN, "x=%p and w=%p must be 16-byte aligned", x, w);
     if ((uintptr_t)idx % 8 || (uintptr_t)vals % 2 || (uintptr_t)y % 2) return fail(KRK_ERR_ALIGN, "idx, vals or y misaligned");
     if (y && ldy < N) return fail(KRK_ERR_INVALID, "ldy=%lld must be >= N=%d", (long long)ldy, N);
-    krk_gemm_config c;
-    if ((rc = select_config(M, N, K, cfg, &c))) return rc;
+    SelectPlan p;
+    if ((rc = select_plan_for(M, N, K, k, cfg, &p))) return rc;
+    const SelectLayout l = select_layout(M, N, k, p);
 
     const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((uint64_t)(M - 1) * ldx + K) * 2;
     const uintptr_t w0 = (uintptr_t)w, w1 = w0 + ((uint64_t)(N - 1) * ldw + K) * 2;
@@ -880,54 +935,78 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
     const uintptr_t v0 = (uintptr_t)vals, v1 = vals ? v0 + (uint64_t)M * k * 2 : v0;
     const uintptr_t y0 = (uintptr_t)y, y1 = y ? y0 + ((uint64_t)(M - 1) * ldy + N) * 2 : y0;
     const uintptr_t s0 = (uintptr_t)workspace;
-    const size_t need = select_workspace(M, N, K, k, c);
-    const uintptr_t s1 = s0 + need;
+    const uintptr_t s1 = s0 + l.total;
     struct Span { uintptr_t a, b; } outs[] = {{i0, i1}, {v0, v1}, {y0, y1}, {s0, s1}};
-    for (int p = 0; p < 4; ++p) {
-        if (outs[p].a == outs[p].b) continue;
-        if (overlaps(outs[p].a, outs[p].b, x0, x1) || overlaps(outs[p].a, outs[p].b, w0, w1))
+    for (int q0 = 0; q0 < 4; ++q0) {
+        if (outs[q0].a == outs[q0].b) continue;
+        if (overlaps(outs[q0].a, outs[q0].b, x0, x1) || overlaps(outs[q0].a, outs[q0].b, w0, w1))
             return fail(KRK_ERR_ALIAS, "outputs and workspace may not share memory with x or W");
-        for (int q = p + 1; q < 4; ++q)
-            if (outs[q].a != outs[q].b && overlaps(outs[p].a, outs[p].b, outs[q].a, outs[q].b))
+        for (int q = q0 + 1; q < 4; ++q)
+            if (outs[q].a != outs[q].b && overlaps(outs[q0].a, outs[q0].b, outs[q].a, outs[q].b))
                 return fail(KRK_ERR_ALIAS, "idx, vals, y and the workspace may not overlap");
     }
-    if (!workspace) return fail(KRK_ERR_WORKSPACE, "token selection needs a %zu-byte workspace, got none", need);
-    if (workspace_bytes < need) return fail(KRK_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, need);
+    if (!workspace) return fail(KRK_ERR_WORKSPACE, "token selection needs a %zu-byte workspace, got none", l.total);
+    if (workspace_bytes < l.total) return fail(KRK_ERR_WORKSPACE, "workspace of %zu bytes < %zu needed", workspace_bytes, l.total);
     if ((uintptr_t)workspace % 256) return fail(KRK_ERR_ALIGN, "workspace=%p must be 256-byte aligned", workspace);
 
     hipStream_t st = static_cast<hipStream_t>(stream);
+    unsigned char* ws = static_cast<unsigned char*>(workspace);
+    const Geometry g = geometry(M, N, KRK_EPILOGUE_NONE, p.c);
     for (int m0 = 0; m0 < M; m0 += kMaxRowsPerLaunch) {
         LaunchArgs a;
         a.x = static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx;
         a.ldx = ldx;
         a.w = static_cast<const uint16_t*>(w);
         a.ldw = ldw;
-        a.y = y ? static_cast<uint16_t*>(y) + (int64_t)m0 * ldy : nullptr;
-        a.ldy = ldy;
         a.M = (M - m0) < kMaxRowsPerLaunch ? (M - m0) : kMaxRowsPerLaunch;
         a.N = N;
         a.K = K;
-        a.splits = 1;
-        a.part = nullptr;
-        a.ctr = nullptr;
-        const Geometry g = geometry(a.M, N, KRK_EPILOGUE_NONE, c);
-        krk::SelectArgs sa{static_cast<unsigned char*>(workspace), idx + (int64_t)m0 * k,
-                           vals ? static_cast<uint16_t*>(vals) + (int64_t)m0 * k : nullptr, k};
-        if (c.kernel == KRK_KERNEL_VALU) {
-            switch (c.m_tiles) {
-                case 1: rc = dispatch_valu_sel<1>(a, c, g.nblocks, st, sa); break;
-                case 2: rc = dispatch_valu_sel<2>(a, c, g.nblocks, st, sa); break;
-                case 4: rc = dispatch_valu_sel<4>(a, c, g.nblocks, st, sa); break;
-                default: rc = fail(KRK_ERR_UNSUPPORTED, "VALU x rows=%d", c.m_tiles);
+        a.splits = p.c.splits;
+        a.ctr = p.c.splits > 1 ? reinterpret_cast<uint32_t*>(ws + l.proj) : nullptr;
+        a.part = p.c.splits > 1 ? reinterpret_cast<float*>(ws + l.proj + align_up((size_t)g.nblocks * sizeof(uint32_t), 256))
+                                : nullptr;
+        krk::RowSelectArgs ra;
+        ra.n = l.n;
+        ra.ctr = reinterpret_cast<uint32_t*>(ws);
+        ra.lists = reinterpret_cast<uint64_t*>(ws + l.lists);
+        ra.idx = idx + (int64_t)m0 * k;
+        ra.vals = vals ? static_cast<uint16_t*>(vals) + (int64_t)m0 * k : nullptr;
+        ra.k = k;
+        if (p.fused) {
+            a.y = y ? static_cast<uint16_t*>(y) + (int64_t)m0 * ldy : nullptr;
+            a.ldy = ldy;
+            const krk::SelectArgs sa{reinterpret_cast<uint64_t*>(ws + l.src), l.ld};
+            if (p.c.kernel == KRK_KERNEL_VALU) {
+                switch (p.c.m_tiles) {
+                    case 1: rc = dispatch_valu_sel<1>(a, p.c, g.nblocks, st, sa); break;
+                    case 2: rc = dispatch_valu_sel<2>(a, p.c, g.nblocks, st, sa); break;
+                    case 4: rc = dispatch_valu_sel<4>(a, p.c, g.nblocks, st, sa); break;
+                    default: rc = fail(KRK_ERR_UNSUPPORTED, "VALU x rows=%d", p.c.m_tiles);
+                }
+            } else {
+                switch (p.c.m_tiles) {
+                    case 1: rc = dispatch_mfma_lds_sel<1>(a, p.c, g.nblocks, st, sa); break;
+                    case 2: rc = dispatch_mfma_lds_sel<2>(a, p.c, g.nblocks, st, sa); break;
+                    case 3: rc = dispatch_mfma_lds_sel<3>(a, p.c, g.nblocks, st, sa); break;
+                    case 4: rc = dispatch_mfma_lds_sel<4>(a, p.c, g.nblocks, st, sa); break;
+                    default: rc = fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", p.c.m_tiles);
+                }
             }
+            if (rc) return rc;
+            ra.src = sa.keys;
+            ra.ld = l.ld;
+            ra.vec = 1;
+            rc = launch_select_rows<1, true>(ra, l.chunks, a.M, st);
         } else {
-            switch (c.m_tiles) {
-                case 1: rc = dispatch_mfma_lds_sel<1>(a, c, g.nblocks, st, sa); break;
-                case 2: rc = dispatch_mfma_lds_sel<2>(a, c, g.nblocks, st, sa); break;
-                case 3: rc = dispatch_mfma_lds_sel<3>(a, c, g.nblocks, st, sa); break;
-                case 4: rc = dispatch_mfma_lds_sel<4>(a, c, g.nblocks, st, sa); break;
-                default: rc = fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
-            }
+            uint16_t* logits = y ? static_cast<uint16_t*>(y) + (int64_t)m0 * ldy : reinterpret_cast<uint16_t*>(ws + l.src);
+            a.y = logits;
+            a.ldy = y ? ldy : l.ld;
+            if ((rc = dispatch_plain(a, p.c, g.nblocks, st))) return rc;
+            ra.src = logits;
+            ra.ld = a.ldy;
+            ra.vec = (a.ldy % 8 == 0) && ((uintptr_t)logits % 16 == 0);
+            rc = k == 1 ? launch_select_rows<1, false>(ra, l.chunks, a.M, st)
+                        : launch_select_rows<krk::kSelMaxK, false>(ra, l.chunks, a.M, st);
         }
         if (rc) return rc;
     }
@@ -1028,17 +1107,31 @@ int krk_gemm_bf16_select_config(const void* x, int64_t ldx, const void* w, int64
 
 size_t krk_gemm_select_workspace_bytes(int M, int N, int K, int k, const krk_gemm_config* cfg) {
     if (check_shape(M, N, K, KRK_EPILOGUE_NONE) || k < 1 || k > krk::kSelMaxK || k > N) return 0;
-    krk_gemm_config c;
-    if (select_config(M, N, K, cfg, &c)) return 0;
-    return select_workspace(M, N, K, k, c);
+    SelectPlan p;
+    if (select_plan_for(M, N, K, k, cfg, &p)) return 0;
+    return select_layout(M, N, k, p).total;
 }
 
-int krk_gemm_select_plan(int M, int N, int K, krk_gemm_config* out) {
+int krk_gemm_select_plan(int M, int N, int K, int k, krk_gemm_config* out) {
     g_err[0] = '\0';
     int rc = check_shape(M, N, K, KRK_EPILOGUE_NONE);
     if (rc) return rc;
+    if (k < 1 || k > krk::kSelMaxK || k > N) return fail(KRK_ERR_INVALID, "k=%d must be in 1..min(%d, N)", k, krk::kSelMaxK);
     if (!out) return fail(KRK_ERR_INVALID, "null output config");
-    return select_config(M, N, K, nullptr, out);
+    SelectPlan p;
+    if ((rc = select_plan_for(M, N, K, k, nullptr, &p))) return rc;
+    *out = p.c;
+    return KRK_OK;
+}
+
+int krk_gemm_select_fused(int M, int N, int K, int k, const krk_gemm_config* cfg) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, KRK_EPILOGUE_NONE);
+    if (rc) return rc;
+    if (k < 1 || k > krk::kSelMaxK || k > N) return fail(KRK_ERR_INVALID, "k=%d must be in 1..min(%d, N)", k, krk::kSelMaxK);
+    SelectPlan p;
+    if ((rc = select_plan_for(M, N, K, k, cfg, &p))) return rc;
+    return p.fused ? 1 : 0;
 }
 
 size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue) {

@@ -56,8 +56,8 @@ __host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool
     return tile > red ? tile : red;
 }
 
-// SEL: token selection (krk_select.h) instead of, or besides, storing y (y may
-// be null); K unsplit.
+// SEL: per-workgroup argmax keys for token selection (krk_select.h) instead
+// of, or besides, storing y (y may be null); K unsplit.
 template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false>
 __global__ void __launch_bounds__(64 * kLdsWaves)
 mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
@@ -234,7 +234,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     if constexpr (SEL) {
         __syncthreads();
         const int n = 16 * NT < Nout - c0 ? 16 * NT : Nout - c0;
-        select_local(sa, selv, 16 * NT, n, c0, M, blockIdx.x, gridDim.x);
+        select_local(sa, selv, 16 * NT, n, c0, M, blockIdx.x);
     } else if (splits > 1) {
         splitk_finish<SILU>(o, ctr, blk, c0, 16 * NH);
     }

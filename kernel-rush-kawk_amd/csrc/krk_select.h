@@ -1,5 +1,5 @@
-// Token selection fused into the lm_head projection: per-row argmax / top-k
-// of the bf16 logits without writing them (gfx950).
+// Token selection after the lm_head projection: per-row argmax / top-k of the
+// bf16 logits (gfx950).
 //
 // Reference consumers: `logits.argmax(dim=-1)` (engine/engine.py:196,
 // engine/model.py:365; lowest index on exact ties, OPTIMIZATION_GUIDE.md:213)
@@ -14,18 +14,20 @@
 // largest value at its lowest index, and keys of distinct indices never tie.
 // Key 0 is below every real key and marks an empty slot.
 //
-// Reduction (no second launch):
-//   * every workgroup writes, per row, the top-k keys of its output channels
-//     to cand[g][m][0..k) (g = its linear index);
-//   * workgroups form groups of kSelGroup; the last one of a group to finish
-//     (agent-scope counter, as the split-K fix-up in krk_epilogue.h) merges
-//     the group's lists into cand2[group][m][0..k);
-//   * the last group to finish merges those lists and writes the indices
-//     (and the values, when asked), then resets the counters for the next
-//     call.
-// A merge of L lists keeps, per row, a subgroup of P threads of one wave: each
-// thread reduces its share of the lists to a sorted local top-k, then k rounds
-// of a subgroup max pick the winners (each round's winner advances its list).
+// Two sources feed select_rows_kernel:
+//   * bf16 logits [M, N] written by a plain projection (top-k, and argmax
+//     where the projection is the stream kernel);
+//   * for argmax behind the VALU and LDS-staged MFMA projections, one key per
+//     row and projection workgroup, written by select_local in the
+//     projection's epilogue (its per-workgroup max costs the projection about
+//     1%, and the logits are never written).
+// select_rows_kernel: workgroup (c, m) reduces chunk c of row m to a sorted
+// list of KM keys (KM = 1 for argmax, kSelMaxK for top-k; each thread keeps a
+// sorted list, the lists meet in an xor tree of bitonic merges), stores it
+// with agent-scope stores and bumps row m's counter; the workgroup that sees
+// the count reach chunks-1 merges the row's lists, writes the row's outputs
+// and resets the counter (the protocol of the split-K fix-up, krk_epilogue.h).
+// A row of one chunk writes its outputs directly.
 #pragma once
 
 #include "krk_epilogue.h"
@@ -33,30 +35,11 @@
 namespace krk {
 
 constexpr int kSelMaxK = 8;
-constexpr int kSelGroup = 256;
-
-// Workspace layout of a selecting call with G workgroups, M rows and k.
-struct SelectLayout {
-    size_t ctr1, ctr2, cand1, cand2, total;
-};
-__host__ __device__ inline SelectLayout select_layout(int G, int M, int k) {
-    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
-    const int ng = (G + kSelGroup - 1) / kSelGroup;
-    SelectLayout l;
-    l.ctr1 = 0;
-    l.ctr2 = al((size_t)ng * 4);
-    l.cand1 = l.ctr2 + 256;
-    l.cand2 = l.cand1 + al((size_t)G * M * k * 8);
-    l.total = l.cand2 + al((size_t)ng * M * k * 8);
-    return l;
-}
-
-struct SelectArgs {
-    unsigned char* ws;   // workspace (select_layout)
-    int64_t* idx;        // [M, k] selected indices
-    uint16_t* vals;      // [M, k] their bf16 values, or null
-    int k;
-};
+constexpr int kSelThreads = 256;
+constexpr int kSelVec = 2;                                // 16-byte loads per thread
+constexpr int kSelChunkVals = kSelThreads * kSelVec * 8;  // bf16 logits per workgroup
+constexpr int kSelChunkKeys = kSelThreads * kSelVec * 2;  // 64-bit keys per workgroup
+constexpr int kSelMaxRows = 64;                           // rows per launch: one counter each
 
 __device__ __forceinline__ uint64_t sel_key(uint32_t bits, uint32_t index) {
     bits &= 0xffffu;
@@ -76,8 +59,10 @@ __device__ __forceinline__ uint16_t sel_bits(uint64_t key) {
     return (uint16_t)((o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu));
 }
 
-// Insert key into a descending list of K keys (a key already present is never
-// offered: keys are unique).
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t umin64(uint64_t a, uint64_t b) { return a > b ? b : a; }
+
+// Insert key into a descending list of K keys (keys are unique).
 template <int K>
 __device__ __forceinline__ void topk_insert(uint64_t (&t)[K], uint64_t key) {
 #pragma unroll
@@ -89,144 +74,224 @@ __device__ __forceinline__ void topk_insert(uint64_t (&t)[K], uint64_t key) {
     }
 }
 
+// a <- the K largest of two descending lists a and b, descending: the
+// elementwise max of a and reversed b is bitonic and holds the K largest;
+// half-cleaners of stride K/2 ... 1 sort it.
+template <int K>
+__device__ __forceinline__ void merge_sorted(uint64_t (&a)[K], const uint64_t (&b)[K]) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) a[i] = umax64(a[i], b[K - 1 - i]);
+#pragma unroll
+    for (int s = K / 2; s >= 1; s >>= 1) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if (i & s) continue;
+            const uint64_t hi = umax64(a[i], a[i + s]);
+            const uint64_t lo = umin64(a[i], a[i + s]);
+            a[i] = hi;
+            a[i + s] = lo;
+        }
+    }
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
     const uint32_t lo = __shfl_xor((uint32_t)v, mask);
     const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), mask);
     return ((uint64_t)hi << 32) | lo;
 }
 
-// Rows per wave and threads per row for M rows over the workgroup's waves.
-__device__ __forceinline__ int sel_threads_per_row(int M, int waves) {
-    const int rows_per_wave = (M + waves - 1) / waves;
-    int p = 64;
-    while (p > 1 && p * rows_per_wave > 64) p >>= 1;
-    return p;
+// Merge the lists of lanes l ^ 1, ..., l ^ (span/2) into every lane's list.
+// Lists longer than one key keep the levels in a loop: the kernels run once
+// per workgroup, so straight-line code would be fetched cold.
+template <int K>
+__device__ __forceinline__ void xor_level(uint64_t (&a)[K], int off) {
+    uint64_t b[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) b[j] = shfl_xor_u64(a[j], off);
+    merge_sorted(a, b);
+}
+template <int K, int SPAN>
+__device__ __forceinline__ void xor_tree(uint64_t (&a)[K]) {
+    if constexpr (K == 1) {
+#pragma unroll
+        for (int off = 1; off < SPAN; off <<= 1) xor_level(a, off);
+    } else {
+#pragma unroll 1
+        for (int off = 1; off < SPAN; off <<= 1) xor_level(a, off);
+    }
 }
 
-// Merge, for every row m < M, the lists src[i][m][0..k) (i < L, row stride
-// M·k keys) into the top k, handed to emit(m, j, key) for j < k.  All threads
-// of the workgroup call this.
-template <typename Emit>
-__device__ void select_merge(const uint64_t* src, int L, int M, int k, Emit emit) {
+// The workgroup's K largest keys, descending, in every lane of wave 0.
+// lds: kSelThreads / 64 * K keys; a barrier separates two calls.
+template <int K>
+__device__ __forceinline__ void block_top(uint64_t (&a)[K], uint64_t* lds) {
+    constexpr int W = kSelThreads / 64;
+    xor_tree<K, 64>(a);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) lds[wave * K + j] = a[j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) a[j] = lds[(lane & (W - 1)) * K + j];
+        xor_tree<K, W>(a);
+    }
+}
+
+// Per-workgroup argmax in the projection's epilogue: for each row m the
+// largest key of the workgroup's bf16 outputs vals[m][0..n) (LDS, row stride
+// ld, channel c0 + i at column i) goes to keys[m * ldk + g].  All threads call
+// this after the outputs are in LDS and a barrier.  Rows spread over the
+// waves; a row takes a subgroup of P lanes (a power of two, no more than the
+// channels need).
+struct SelectArgs {
+    uint64_t* keys;  // [M, ldk] one key per row and projection workgroup
+    int64_t ldk;
+};
+
+__device__ void select_local(const SelectArgs& sa, const uint16_t* vals, int ld, int n, int c0, int M, int g) {
     const int waves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int P = sel_threads_per_row(M, waves);
-    const int rows_per_wave = 64 / P;
-    const int sub = lane / P;       // subgroup in the wave
-    const int t = lane - sub * P;   // thread in the subgroup
-    for (int m0 = 0; m0 < M; m0 += waves * rows_per_wave) {
-        const int m = m0 + wave * rows_per_wave + sub;
-        const bool live = m < M;
-        uint64_t top[kSelMaxK];
+    const int rows = (M + waves - 1) / waves;  // rows per wave
+    int P = 64;
+    while (P > 1 && P * rows > 64) P >>= 1;
+    while (P > 1 && (P >> 1) >= n) P >>= 1;
+    const int sub = lane / P;
+    const int t = lane - sub * P;
+    for (int m0 = 0; m0 < M; m0 += waves * (64 / P)) {
+        const int m = m0 + wave * (64 / P) + sub;
+        uint64_t best = 0;
+        if (m < M)
+            for (int i = t; i < n; i += P) best = umax64(best, sel_key(vals[m * ld + i], (uint32_t)(c0 + i)));
+        for (int off = 1; off < P; off <<= 1) best = umax64(best, shfl_xor_u64(best, off));
+        if (m < M && t == 0) sa.keys[(int64_t)m * sa.ldk + g] = best;
+    }
+}
+
+struct RowSelectArgs {
+    const void* src;   // [M, ld]: bf16 logits, or 64-bit keys
+    int64_t ld;
+    int n;             // elements of a row
+    int vec;           // rows 16-byte aligned: whole vectors are loaded at once
+    uint32_t* ctr;     // [kSelMaxRows] row counters, zero between calls
+    uint64_t* lists;   // [M, chunks, k] per-chunk winners
+    int64_t* idx;      // [M, k] selected indices (-1: empty)
+    uint16_t* vals;    // [M, k] their bf16 values, or null
+    int k;
+};
+
+__device__ __forceinline__ void store_agent_u64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Grid (chunks, M): KM = 1 (argmax) or kSelMaxK (top-k, k <= KM); KEYS: src
+// holds keys (argmax only) instead of bf16 logits.
+template <int KM, bool KEYS>
+__global__ void __launch_bounds__(kSelThreads) select_rows_kernel(RowSelectArgs a) {
+    static_assert(!KEYS || KM == 1, "key sources carry one key per row and workgroup");
+    __shared__ uint64_t lds[kSelThreads / 64 * KM];
+    __shared__ int last;
+    const int c = blockIdx.x;
+    const int m = blockIdx.y;
+    const int C = gridDim.x;
+    const int t = threadIdx.x;
+    uint64_t top[KM];
 #pragma unroll
-        for (int j = 0; j < kSelMaxK; ++j) top[j] = 0;
-        if (live) {
-            for (int i = t; i < L; i += P) {
-                const uint64_t* lst = src + ((size_t)i * M + m) * k;
-                for (int j = 0; j < k; ++j) {
-                    const uint64_t key = __hip_atomic_load(lst + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (key <= top[kSelMaxK - 1]) break;  // the list is descending
-                    topk_insert(top, key);
+    for (int j = 0; j < KM; ++j) top[j] = 0;
+
+    if constexpr (KEYS) {
+        const uint64_t* row = static_cast<const uint64_t*>(a.src) + (int64_t)m * a.ld;
+        uint64_t v[kSelVec][2];
+#pragma unroll
+        for (int u = 0; u < kSelVec; ++u) {
+            const int64_t e = (int64_t)c * kSelChunkKeys + 2 * (u * kSelThreads + t);
+            if (a.vec && e + 2 <= a.n) {
+                const u32x4 q = *reinterpret_cast<const u32x4*>(row + e);
+                v[u][0] = ((uint64_t)q[1] << 32) | q[0];
+                v[u][1] = ((uint64_t)q[3] << 32) | q[2];
+            } else {
+                v[u][0] = e < a.n ? row[e] : 0;
+                v[u][1] = e + 1 < a.n ? row[e + 1] : 0;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kSelVec; ++u) top[0] = umax64(top[0], umax64(v[u][0], v[u][1]));
+    } else {
+        const uint16_t* row = static_cast<const uint16_t*>(a.src) + (int64_t)m * a.ld;
+        u32x4 v[kSelVec];
+        int64_t e0[kSelVec];
+#pragma unroll
+        for (int u = 0; u < kSelVec; ++u) {
+            e0[u] = (int64_t)c * kSelChunkVals + 8 * (u * kSelThreads + t);
+            if (a.vec && e0[u] + 8 <= a.n) {
+                v[u] = *reinterpret_cast<const u32x4*>(row + e0[u]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t lo = e0[u] + 2 * j < a.n ? row[e0[u] + 2 * j] : 0u;
+                    const uint32_t hi = e0[u] + 2 * j + 1 < a.n ? row[e0[u] + 2 * j + 1] : 0u;
+                    v[u][j] = lo | (hi << 16);
                 }
             }
         }
-        // k rounds of a subgroup max; the winner's thread advances its list.
-        int head = 0;
-        for (int j = 0; j < k; ++j) {
-            uint64_t mine = 0;
 #pragma unroll
-            for (int q = 0; q < kSelMaxK; ++q) mine = (q == head) ? top[q] : mine;
-            uint64_t best = mine;
-            for (int off = 1; off < P; off <<= 1) {
-                const uint64_t o = shfl_xor_u64(best, off);
-                best = o > best ? o : best;
+        for (int u = 0; u < kSelVec; ++u) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t e = e0[u] + j;
+                const uint64_t key = e < a.n ? sel_key(v[u][j >> 1] >> (16 * (j & 1)), (uint32_t)e) : 0;
+                if constexpr (KM == 1) top[0] = umax64(top[0], key);
+                else topk_insert(top, key);
             }
-            if (live && mine == best && best != 0) ++head;
-            if (live && t == 0) emit(m, j, best);
         }
     }
-}
+    block_top(top, lds);
 
-// Called by every thread of a workgroup once its per-row top-k lists are in
-// cand1 (written by the caller as slot g).  Runs the group and final merges.
-__device__ void select_finish(const SelectArgs& sa, int g, int G, int M) {
-    __shared__ int stage;
-    const SelectLayout l = select_layout(G, M, sa.k);
-    uint32_t* ctr1 = reinterpret_cast<uint32_t*>(sa.ws + l.ctr1);
-    uint32_t* ctr2 = reinterpret_cast<uint32_t*>(sa.ws + l.ctr2);
-    uint64_t* cand1 = reinterpret_cast<uint64_t*>(sa.ws + l.cand1);
-    uint64_t* cand2 = reinterpret_cast<uint64_t*>(sa.ws + l.cand2);
-    const int ng = (G + kSelGroup - 1) / kSelGroup;
-    const int grp = g / kSelGroup;
-    const int gsize = (grp + 1) * kSelGroup <= G ? kSelGroup : G - grp * kSelGroup;
-
-    drain_memory();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(ctr1 + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        stage = prev == (uint32_t)(gsize - 1);
-    }
-    __syncthreads();
-    if (!stage) return;
-    // Last of its group: merge the group's lists.
-    select_merge(cand1 + (size_t)grp * kSelGroup * M * sa.k, gsize, M, sa.k, [&](int m, int j, uint64_t key) {
-        __hip_atomic_store(cand2 + ((size_t)grp * M + m) * sa.k + j, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    });
-    drain_memory();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(ctr1 + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t prev = __hip_atomic_fetch_add(ctr2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        stage = prev == (uint32_t)(ng - 1);
-    }
-    __syncthreads();
-    if (!stage) return;
-    // Last group: final merge and the outputs.
-    select_merge(cand2, ng, M, sa.k, [&](int m, int j, uint64_t key) {
-        sa.idx[(int64_t)m * sa.k + j] = key ? (int64_t)sel_index(key) : -1;
-        if (sa.vals) sa.vals[(int64_t)m * sa.k + j] = key ? sel_bits(key) : (uint16_t)0xff80u;  // empty: -inf
-    });
-    if (threadIdx.x == 0) __hip_atomic_store(ctr2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Per-row top-k of the workgroup's own bf16 outputs vals[m][0..n) (LDS, row
-// stride ld, channel c0 + i at column i), written as list g of cand1.  All
-// threads call this after the outputs are in LDS and a barrier.
-__device__ void select_local(const SelectArgs& sa, const uint16_t* vals, int ld, int n, int c0, int M, int g, int G) {
-    const SelectLayout l = select_layout(G, M, sa.k);
-    uint64_t* cand1 = reinterpret_cast<uint64_t*>(sa.ws + l.cand1) + (size_t)g * M * sa.k;
-    const int waves = blockDim.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int P = sel_threads_per_row(M, waves);
-    const int rows_per_wave = 64 / P;
-    const int sub = lane / P;
-    const int t = lane - sub * P;
-    for (int m0 = 0; m0 < M; m0 += waves * rows_per_wave) {
-        const int m = m0 + wave * rows_per_wave + sub;
-        const bool live = m < M;
-        uint64_t top[kSelMaxK];
+    auto emit = [&](const uint64_t (&r)[KM]) {
 #pragma unroll
-        for (int j = 0; j < kSelMaxK; ++j) top[j] = 0;
-        if (live)
-            for (int i = t; i < n; i += P) topk_insert(top, sel_key(vals[m * ld + i], (uint32_t)(c0 + i)));
-        int head = 0;
-        for (int j = 0; j < sa.k; ++j) {
-            uint64_t mine = 0;
-#pragma unroll
-            for (int q = 0; q < kSelMaxK; ++q) mine = (q == head) ? top[q] : mine;
-            uint64_t best = mine;
-            for (int off = 1; off < P; off <<= 1) {
-                const uint64_t o = shfl_xor_u64(best, off);
-                best = o > best ? o : best;
-            }
-            if (live && mine == best && best != 0) ++head;
-            if (live && t == 0)
-                __hip_atomic_store(cand1 + (size_t)m * sa.k + j, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < KM; ++j) {
+            if (j >= a.k) break;
+            a.idx[(int64_t)m * a.k + j] = r[j] ? (int64_t)sel_index(r[j]) : -1;
+            if (a.vals) a.vals[(int64_t)m * a.k + j] = r[j] ? sel_bits(r[j]) : (uint16_t)0xff80u;  // empty: -inf
         }
+    };
+    if (C == 1) {
+        if (t == 0) emit(top);
+        return;
     }
-    select_finish(sa, g, G, M);
+    if (t == 0) {
+        uint64_t* dst = a.lists + ((int64_t)m * C + c) * a.k;
+#pragma unroll
+        for (int j = 0; j < KM; ++j)
+            if (j < a.k) store_agent_u64(dst + j, top[j]);
+        drain_memory();
+        const uint32_t prev = __hip_atomic_fetch_add(a.ctr + m, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == (uint32_t)(C - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    // The row's last workgroup: merge the C sorted lists.
+#pragma unroll
+    for (int j = 0; j < KM; ++j) top[j] = 0;
+    for (int i = t; i < C; i += kSelThreads) {
+        const uint64_t* src = a.lists + ((int64_t)m * C + i) * a.k;
+        uint64_t b[KM];
+#pragma unroll
+        for (int j = 0; j < KM; ++j) b[j] = j < a.k ? load_agent_u64(src + j) : 0;
+        merge_sorted(top, b);
+    }
+    block_top(top, lds);
+    if (t == 0) {
+        emit(top);
+        __hip_atomic_store(a.ctr + m, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 }  // namespace krk

@@ -138,8 +138,8 @@ constexpr int log2_exact() {
 // covers waves * R (SILU: waves * R/2) consecutive output channels.  Split s
 // owns K blocks [s*per + min(s, rem), ...) where per = nb / splits and
 // rem = nb % splits (nb = ceil(K / 512)), so no division runs on the device.
-// SEL: token selection (krk_select.h) instead of, or besides, storing y (y may
-// be null); K unsplit.
+// SEL: per-workgroup argmax keys for token selection (krk_select.h) instead
+// of, or besides, storing y (y may be null); K unsplit.
 template <int MX, int R, int D, bool SILU, bool EXACT, bool NORM = false, bool SEL = false>
 __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w, int64_t ldw,
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
         if ((lane & (G - 1)) == 0 && r < RO) selv[m * cb + wave * RO + r] = (uint16_t)f32_to_bf16(acc[0]);
         if (y && (lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
         __syncthreads();
-        select_local(sa, selv, cb, cb < Nout - c0 ? cb : Nout - c0, c0, M, blk, gridDim.x);
+        select_local(sa, selv, cb, cb < Nout - c0 ? cb : Nout - c0, c0, M, blk);
     } else {
         if ((lane & (G - 1)) == 0 && m < M && r < RO && c < Nout) o.put(m, c, acc[0], u);
         if (splits > 1) splitk_finish<SILU, 4, 1>(o, ctr, blk, c0, cb);

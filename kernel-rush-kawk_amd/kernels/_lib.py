@@ -91,7 +91,8 @@ SIGNATURES = {
                                             _c_void_p, _c_void_p, ctypes.POINTER(GemmConfig), _c_void_p, _size,
                                             _c_void_p]),
     "krk_gemm_select_workspace_bytes": (_size, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
-    "krk_gemm_select_plan": (_int, [_int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_select_plan": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_select_fused": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_last_error": (ctypes.c_char_p, []),
 }
 

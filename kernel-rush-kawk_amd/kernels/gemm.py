@@ -35,7 +35,7 @@ from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "SkinnySelect", "pick_matmul", "pick_gateup", "pick_normed",
-    "add_rms_norm", "plan", "select_plan", "gemm_into", "normed_fused", "_time",
+    "add_rms_norm", "plan", "select_plan", "select_fused", "gemm_into", "normed_fused", "_time",
 ]
 
 
@@ -393,20 +393,34 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
     return fn
 
 
-def select_plan(M: int, N: int, K: int) -> dict:
-    """The configuration a selecting lm_head call uses for this shape."""
+def select_plan(M: int, N: int, K: int, k: int = 1) -> dict:
+    """The projection configuration a selecting lm_head call uses for this
+    shape and k."""
     cfg = GemmConfig()
-    _lib.check(_lib.load().krk_gemm_select_plan(M, N, K, ctypes.byref(cfg)))
+    _lib.check(_lib.load().krk_gemm_select_plan(M, N, K, k, ctypes.byref(cfg)))
     return cfg.as_dict()
 
 
+def select_fused(M: int, N: int, K: int, k: int = 1, config: dict | None = None) -> bool:
+    """Whether the selection runs in the projection's epilogue (argmax behind
+    a VALU or LDS-staged MFMA projection: the logits are then not written
+    unless asked for) rather than in a kernel that reads the logits back."""
+    cfg = GemmConfig.from_dict(config) if config else None
+    rc = _lib.load().krk_gemm_select_fused(M, N, K, k, ctypes.byref(cfg) if cfg else None)
+    _lib.check(min(rc, 0))
+    return rc == 1
+
+
 class SkinnySelect:
-    """The lm_head projection with token selection fused: ``f(a, w)`` returns
+    """The lm_head projection followed by token selection: ``f(a, w)`` returns
     the ``[M, k]`` int64 indices of each row's k largest bf16 logits of
     ``a @ w.T`` (largest first, equal values at the lower index first, NaN
-    above everything), without writing the logits unless ``logits`` is given.
-    ``k = 1`` is ``(a @ w.T).argmax(dim=-1, keepdim=True)`` (engine/engine.py:196),
-    ``k = 8`` the ``torch.topk(logits, 8).indices`` of engine/recycle.py:170.
+    above everything).  ``k = 1`` is ``(a @ w.T).argmax(dim=-1, keepdim=True)``
+    (engine/engine.py:196), ``k = 8`` the ``torch.topk(logits, 8).indices`` of
+    engine/recycle.py:170.  Argmax behind the VALU and LDS-staged MFMA plans
+    runs in the projection's epilogue (``fused``) and writes no logits unless
+    ``logits`` is given; other plans write the logits and select from them.
+    ``config`` is the projection's configuration (any plain-epilogue one).
     The workspace belongs to the object (zero-filled once; calls leave it so)."""
 
     def __init__(self, M: int, N: int, K: int, device, k: int = 1, config: dict | None = None):
@@ -418,13 +432,17 @@ class SkinnySelect:
         cfg = GemmConfig.from_dict(config) if config else None
         nbytes = int(_lib.load().krk_gemm_select_workspace_bytes(M, N, K, k, ctypes.byref(cfg) if cfg else None))
         if nbytes == 0:
-            raise ValueError(f"no token-selection plan for M={M} N={N} K={K} k={k} config={config}: "
+            raise ValueError(f"invalid token selection M={M} N={N} K={K} k={k} config={config}: "
                              f"{_lib.last_error() or 'k must be 1..8 and <= N'}")
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
 
     @property
     def resolved_config(self) -> dict:
-        return dict(self.config) if self.config else select_plan(self.M, self.N, self.K)
+        return dict(self.config) if self.config else select_plan(self.M, self.N, self.K, self.k)
+
+    @property
+    def fused(self) -> bool:
+        return select_fused(self.M, self.N, self.K, self.k, self.config)
 
     def run(self, a: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, logits: torch.Tensor | None = None,
             values: torch.Tensor | None = None) -> torch.Tensor:

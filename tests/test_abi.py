@@ -305,7 +305,7 @@ def test_add_rms_norm_argument_errors(lib, kw, code):
     assert rc == code, _lib.last_error()
 
 
-# ------------------------------------------------------------------ fused token selection
+# ------------------------------------------------------------------ token selection
 
 # The lm_head weight spans 778 MB: select calls keep everything else far from it.
 W_LM, IDX, WS_SEL, Y_SEL = 0x100000000, 0x300000000, 0x400000000, 0x500000000
@@ -337,23 +337,44 @@ def test_select_argument_errors(lib, kw, code, msg):
 
 
 def test_select_plan_and_workspace(lib):
-    """VALU plans up to M = 4, the LDS-staged MFMA kernel with 256-k stages
-    beyond (never the persistent stream kernel); the workspace holds one
-    candidate list per workgroup and per group of 256."""
+    """The projection plan is the plain table's; argmax fuses into the VALU
+    (M <= 4) and LDS-staged MFMA (M <= 16) plans, never into the stream
+    kernel (M >= 17) or a top-k.  Workspace: the row counters, then the
+    per-workgroup keys (fused) or a logits buffer, then the per-chunk lists."""
+    al = lambda v: -(-v // 256) * 256
+    N, K = 151936, 2560
     for M, kernel in [(1, _lib.KERNEL_VALU), (4, _lib.KERNEL_VALU), (5, _lib.KERNEL_MFMA_LDS),
-                      (32, _lib.KERNEL_MFMA_LDS), (64, _lib.KERNEL_MFMA_LDS), (100, _lib.KERNEL_MFMA_LDS)]:
-        cfg = GemmConfig()
-        assert lib.krk_gemm_select_plan(M, 151936, 2560, ctypes.byref(cfg)) == 0
-        c = cfg.as_dict()
-        assert c["kernel"] == kernel and c["splits"] == 1, (M, c)
-        if kernel == _lib.KERNEL_MFMA_LDS:
-            assert c["k_chunk"] == 256
+                      (16, _lib.KERNEL_MFMA_LDS), (17, _lib.KERNEL_STREAM), (64, _lib.KERNEL_STREAM),
+                      (100, _lib.KERNEL_STREAM)]:
         Mc = min(M, 64)
-        G = -(-151936 // _channels_per_block(c, NONE))
-        ng = -(-G // 256)
-        al = lambda v: -(-v // 256) * 256
         for k in (1, 8):
-            want = al(ng * 4) + 256 + al(G * Mc * k * 8) + al(ng * Mc * k * 8)
-            assert lib.krk_gemm_select_workspace_bytes(M, 151936, 2560, k, None) == want
-    bad = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_STREAM))
-    assert lib.krk_gemm_select_workspace_bytes(32, 151936, 2560, 1, ctypes.byref(bad)) == 0
+            cfg, plain = GemmConfig(), GemmConfig()
+            assert lib.krk_gemm_select_plan(M, N, K, k, ctypes.byref(cfg)) == 0
+            assert lib.krk_gemm_plan(M, N, K, NONE, ctypes.byref(plain)) == 0
+            c = cfg.as_dict()
+            assert c == plain.as_dict() and c["kernel"] == kernel, (M, k, c)
+            fused = lib.krk_gemm_select_fused(M, N, K, k, None)
+            assert fused == int(k == 1 and kernel != _lib.KERNEL_STREAM), (M, k)
+            if fused:
+                G = -(-N // _channels_per_block(c, NONE))
+                src = al(Mc * (-(-G // 2) * 2) * 8)  # one key per row and workgroup
+                chunks = -(-G // 1024)
+            else:
+                src = al(Mc * (-(-N // 8) * 8) * 2)  # bf16 logits
+                chunks = -(-N // 4096)
+            want = 256 + src + al(Mc * chunks * k * 8)
+            assert lib.krk_gemm_select_workspace_bytes(M, N, K, k, None) == want, (M, k)
+    # Any plain configuration is accepted: the stream kernel writes logits.
+    stream = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_STREAM))
+    assert lib.krk_gemm_select_workspace_bytes(8, N, K, 1, ctypes.byref(stream)) > 0
+    assert lib.krk_gemm_select_fused(8, N, K, 1, ctypes.byref(stream)) == 0
+    # A split-K projection reserves its partials after the counters.
+    split = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_VALU, splits=2))
+    c = GemmConfig()
+    assert lib.krk_gemm_select_fused(1, N, K, 1, ctypes.byref(split)) == 0
+    assert lib.krk_gemm_select_workspace_bytes(1, N, K, 1, ctypes.byref(split)) > \
+        lib.krk_gemm_select_workspace_bytes(1, N, K, 1, ctypes.byref(stream))
+    assert lib.krk_gemm_select_fused(1, N, K, 9, None) == _lib.KRK_ERR_INVALID
+    assert lib.krk_gemm_select_plan(1, N, K, 0, ctypes.byref(c)) == _lib.KRK_ERR_INVALID
+    bad = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_MFMA_LDS, k_chunk=384))
+    assert lib.krk_gemm_select_workspace_bytes(32, N, K, 1, ctypes.byref(bad)) == 0

@@ -647,7 +647,7 @@ def test_pick_normed_returns_validated_callable(device):
     assert g(x, y, wn, xo, wgu).shape == (M, 9728)
 
 
-# ------------------------------------------------------------------ fused token selection (lm_head argmax / top-k)
+# ------------------------------------------------------------------ token selection (lm_head argmax / top-k)
 
 def krk_select(x, w, k, config=None, logits=True, device="cuda:0", wd=None):
     """Selecting HIP call on CPU inputs; returns (idx, vals, logits or None) on the CPU."""
@@ -694,7 +694,8 @@ def test_select_lm_head(device, lm_head, lm_head_dev, M, k):
     if k == 1:
         assert torch.equal(idx[:, 0], R.argmax_rows(ref)), f"select M={M}: argmax differs from the oracle's"
     idx2, vals2, _ = krk_select(x, lm_head, k, logits=False, wd=lm_head_dev)
-    assert torch.equal(idx, idx2) and torch.equal(vals, vals2), "selection without logits differs"
+    assert torch.equal(idx, idx2) and torch.equal(vals.view(torch.int16), vals2.view(torch.int16)), \
+        "selection without logits differs"
 
 
 def _tie_weights(N, K, seed):
@@ -709,7 +710,8 @@ def _tie_weights(N, K, seed):
                                    (33, 5000, 2560), (64, 257, 1024)])
 def test_select_ties_nan_and_configs(device, M, N, K):
     """Equal logits (repeated W rows) rank the lower index first; a NaN logit
-    ranks above everything; every selection configuration agrees bit for bit."""
+    ranks above everything; every projection configuration, fused or not,
+    with or without caller logits, selects the same indices bit for bit."""
     x = R.randn_bf16((M, K), 9900 + M)
     w = _tie_weights(N, K, 9901 + N)
     w[N // 2, 0] = float("nan")         # logits of row N//2 are NaN in every row m
@@ -719,20 +721,24 @@ def test_select_ties_nan_and_configs(device, M, N, K):
                  for nt in (1, 2, 4) for wv in (1, 4, 8)]
     cfgs += [dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=nt, unroll=pf, k_chunk=256, splits=1)
              for nt in (2, 4) for pf in (2, 3)]
-    base = None
+    cfgs += [dict(kernel=_lib.KERNEL_STREAM), dict(kernel=_lib.KERNEL_VALU, splits=2),
+             dict(kernel=_lib.KERNEL_MFMA, splits=1)]
+    base = {}
     for cfg in cfgs:
         for k in (1, 8):
             say("select ties", M, N, K, k, cfg)
             try:
                 idx, vals, logits = krk_select(x, w, k, cfg)
             except ValueError as e:  # a combination the library does not provide (e.g. unroll 3 on big tiles)
-                assert cfg is not None and "no token-selection plan" in str(e), e
+                assert cfg is not None and "invalid token selection" in str(e), e
                 continue
             _check_selection(idx, vals, logits, k, f"select {cfg} k={k}")
             assert (idx[:, 0] == N // 2).all(), "the NaN logit must rank first"
-            if k == 8:
-                base = idx if base is None else base
-                assert torch.equal(idx, base), f"select {cfg}: differs from the first configuration"
+            base.setdefault(k, idx)
+            assert torch.equal(idx, base[k]), f"select {cfg} k={k}: differs from the first configuration"
+            idx2, vals2, _ = krk_select(x, w, k, cfg, logits=False)
+            assert torch.equal(idx, idx2) and torch.equal(vals.view(torch.int16), vals2.view(torch.int16)), \
+                f"select {cfg} k={k}: differs without logits"
 
 
 def test_select_graph_replay(device, lm_head_dev):
