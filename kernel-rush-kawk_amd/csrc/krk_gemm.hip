@@ -872,7 +872,7 @@ int select_plan_for(int M, int N, int K, int k, const krk_gemm_config* cfg, Sele
 
 // Workspace of a selecting call, for one launch of Mc rows (launches of a
 // call run in order on one stream and reuse it):
-//   [row counters, 256 B][projection split-K area][keys [Mc, ldk] u64 (fused)
+//   [row counters, 128 B apart][projection split-K area][keys [Mc, ldk] u64 (fused)
 //    or logits [Mc, ldl] bf16 (unfused; unused when the caller passes y)]
 //   [chunk lists [Mc, C, k]]
 struct SelectLayout {
@@ -884,7 +884,7 @@ struct SelectLayout {
 SelectLayout select_layout(int M, int N, int k, const SelectPlan& p) {
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     SelectLayout l;
-    l.proj = 256;
+    l.proj = (size_t)krk::kSelMaxRows * krk::kSelCtrStride * sizeof(uint32_t);
     size_t at = align_up(l.proj + workspace_for(Mc, N, KRK_EPILOGUE_NONE, p.c), 256);
     l.src = at;
     if (p.fused) {

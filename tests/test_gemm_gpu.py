@@ -707,11 +707,13 @@ def _tie_weights(N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1000, 2560), (3, 4099, 2560), (4, 300, 2560), (7, 1000, 512),
-                                   (33, 5000, 2560), (64, 257, 1024)])
+                                   (33, 5000, 2560), (64, 257, 1024), (2, 600001, 64)])
 def test_select_ties_nan_and_configs(device, M, N, K):
     """Equal logits (repeated W rows) rank the lower index first; a NaN logit
     ranks above everything; every projection configuration, fused or not,
-    with or without caller logits, selects the same indices bit for bit."""
+    with or without caller logits, selects the same indices bit for bit.
+    N = 600001 has more than 32 chunks of logits per row, so a row's chunk
+    lists exceed the LDS ranking and merge through sorted-list trees."""
     x = R.randn_bf16((M, K), 9900 + M)
     w = _tie_weights(N, K, 9901 + N)
     w[N // 2, 0] = float("nan")         # logits of row N//2 are NaN in every row m
