@@ -314,6 +314,91 @@ def main() -> int:
                 log(f"select M={Mt:3d} k={k}  {'fused' if op.fused else 'logits'} {row['us']:8.2f} us   lm_head + torch "
                     f"{'argmax' if k == 1 else 'topk'} {row['plain_gemm_plus_torch_select_us']:8.2f} us")
 
+    # ------------------------------------------------------------ decode step through the engine adapter
+    # The 145 projection calls of one decode step as the reference engine
+    # issues them (engine/model.py:181-214): kernels.step.decode_matmuls
+    # builds the engine's mm dict on the library (normed qkv / gate_up /
+    # lm_head, plain o / down), GemmStep runs the residual data flow over the
+    # 36 layer weights and is captured in one graph.  Reported: µs per step,
+    # the sum of the same calls timed in isolation (each call type in its own
+    # graph over the 36 layer weights), their difference per call (the gap
+    # between consecutive launches in a replayed step), and the torch
+    # composition of the same step (F.linear + torch norm / SwiGLU ops).
+    step_rows = []
+    if not args.no_table:
+        from types import SimpleNamespace
+
+        from kernels import step as S
+
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(4321)
+        gain = lambda: torch.randn((HIDDEN,), generator=gen, device=dev).mul_(0.1).add_(1.0).to(torch.bfloat16)
+        cfg = S.QwenConfig()
+        model = SimpleNamespace(cfg=cfg, device=dev, lm_head=lm[0], final_norm=gain(),
+                                layers=[SimpleNamespace(in_norm=gain(), wqkv=L["qkv"], wo=L["o"], post_norm=gain(),
+                                                        wgu=L["gate_up"], wd=L["down"]) for L in layers])
+        eps = cfg.eps
+        for Mt in (1, 32):
+            st = S.GemmStep(model, Mt)
+            xs = randn_bf16(torch, (Mt, HIDDEN), 501 + Mt, 1.0, dev)
+            st.attn_out.copy_(randn_bf16(torch, tuple(st.attn_out.shape), 502 + Mt, 1.0, dev))
+            st.capture(xs)
+            for _ in range(3):
+                st.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            e0.record()
+            for _ in range(reps):
+                st.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            step_us = e0.elapsed_time(e1) / reps * 1000
+            mm = st.mm
+            xo = torch.empty((Mt, HIDDEN), dtype=torch.bfloat16, device=dev)
+            yy = randn_bf16(torch, (Mt, HIDDEN), 503 + Mt, 1.0, dev)
+            act = randn_bf16(torch, (Mt, INTER), 504 + Mt, 1.0, dev)
+            per = {
+                "qkv": [(lambda Lm=Lm: mm["qkv"](xs, yy, Lm.in_norm, xo, Lm.wqkv)) for Lm in model.layers],
+                "o": [(lambda Lm=Lm: mm["o"](st.attn_out, Lm.wo)) for Lm in model.layers],
+                "gu": [(lambda Lm=Lm: mm["gu"](xs, yy, Lm.post_norm, xo, Lm.wgu)) for Lm in model.layers],
+                "d": [(lambda Lm=Lm: mm["d"](act, Lm.wd)) for Lm in model.layers],
+                "lm": [(lambda w=w: mm["lm"](xs, yy, model.final_norm, xo, w)) for w in lm * 4],
+            }
+            iso = {k: graph_time_ms(torch, v)[0] * 1000 for k, v in per.items()}
+            iso_sum = LAYERS * (iso["qkv"] + iso["o"] + iso["gu"] + iso["d"]) + iso["lm"]
+            row = {"M": Mt, "calls": st.calls, "us_per_step": round(step_us, 1),
+                   "isolated_sum_us": round(iso_sum, 1),
+                   "gap_us_per_call": round((step_us - iso_sum) / st.calls, 3),
+                   "isolated_us": {k: round(v, 2) for k, v in iso.items()}}
+            if not args.no_torch:
+                def rms(xx, yv, wn, xout):
+                    s_ = (xx.float() + yv.float()).to(torch.bfloat16)
+                    xout.copy_(s_)
+                    sf = s_.float()
+                    r_ = torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + eps)
+                    return ((sf * r_).to(torch.bfloat16).float() * wn.float()).to(torch.bfloat16)
+
+                def torch_step():
+                    xa_, xb_ = st.xa, st.xb
+                    cur, yv = xs, st.zero
+                    for Lm in model.layers:
+                        F.linear(rms(cur, yv, Lm.in_norm, xa_), Lm.wqkv)
+                        o_ = F.linear(st.attn_out, Lm.wo)
+                        gu_ = F.linear(rms(xa_, o_, Lm.post_norm, xb_), Lm.wgu)
+                        yv = F.linear(F.silu(gu_[:, :INTER]) * gu_[:, INTER:], Lm.wd)
+                        cur = xb_
+                    return F.linear(rms(cur, yv, model.final_norm, xa_), model.lm_head)
+
+                tms, _ = graph_time_ms(torch, [torch_step], reps=5)
+                row["torch_us_per_step"] = round(tms * 1000, 1)
+            step_rows.append(row)
+            log(f"decode step M={Mt:3d}: {row['us_per_step']:8.1f} us/step ({st.calls} calls), isolated sum "
+                f"{row['isolated_sum_us']:8.1f} us, gap {row['gap_us_per_call']:.2f} us/call"
+                + (f", torch {row['torch_us_per_step']:8.1f} us/step" if "torch_us_per_step" in row else ""))
+            del st
+        del model
+
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if not args.no_cpu:
@@ -343,6 +428,7 @@ def main() -> int:
         "per_gemm": table,
         "normed": normed,
         "select": select,
+        "decode_step": step_rows,
     }
     print(json.dumps(result), flush=True)
     return 0

@@ -129,6 +129,19 @@ typedef struct krk_gemm_config {
 int krk_gemm_plan(int M, int N, int K, int epilogue, krk_gemm_config* out);
 
 /*
+ * krk_gemm_candidates — the search space of a warm-up tuner for this shape:
+ * every distinct configuration the library accepts from a fixed grid (VALU
+ * rows per wave x waves x splits for M <= 8, LDS-staged MFMA tiles x stages
+ * in flight x k per stage x splits, stream kernel depth x splits, register
+ * MFMA tiles x splits), resolved as krk_gemm_bf16_config would resolve it,
+ * krk_gemm_plan's configuration first.  Writes the first cap of them to out
+ * and returns how many there are (negative on an invalid shape).  Stands in
+ * for the GEMV_CONFIGS / CONFIGS lists the reference's pickers try
+ * (engine/kernels/gemm.py:284, 364-375, used at 417-458).
+ */
+int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out, int cap);
+
+/*
  * krk_gemm_config_workspace_bytes — as krk_gemm_workspace_bytes, for an
  * explicit configuration (0 fields filled from krk_gemm_plan).
  */

@@ -82,8 +82,10 @@ Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
 // The dispatch table.  Every projection is HBM-bound (arithmetic intensity is
 // about M flop/byte), so the table only decides how the weight stream is cut.
 // Entries for the five Qwen3-4B projections were chosen by timing every
-// configuration on an MI355X (graph replay over 24 distinct weight copies);
-// other shapes use the rule in auto_config below.
+// configuration on an MI355X (graph replay over 24 distinct weight copies),
+// then checked against the warm-up tuner's search over krk_gemm_candidates
+// (entries it beat by 3% or more were replaced); other shapes use the rule in
+// auto_config below.
 struct TableEntry {
     int N, K, epilogue, m_lo, m_hi;
     krk_gemm_config cfg;  // m_tiles 0: derived from M
@@ -105,9 +107,10 @@ const TableEntry kTable[] = {
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 17, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 25, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
@@ -115,9 +118,11 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 2, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 2, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // lm_head 2560 -> 151936
-    {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256)},
@@ -1155,6 +1160,44 @@ int krk_gemm_plan(int M, int N, int K, int epilogue, krk_gemm_config* out) {
     if (!out) return fail(KRK_ERR_INVALID, "null output config");
     auto_config(M, N, K, epilogue, out);
     return KRK_OK;
+}
+
+int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out, int cap) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    if (cap < 0 || (cap > 0 && !out)) return fail(KRK_ERR_INVALID, "need an output array for cap=%d configurations", cap);
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    constexpr int kMax = 256;
+    krk_gemm_config found[kMax];
+    int n = 0;
+    auto add = [&](const krk_gemm_config& want) {
+        krk_gemm_config r;
+        if (resolve_config(M, N, K, epilogue, &want, &r)) return;
+        for (int i = 0; i < n; ++i)
+            if (!memcmp(&found[i], &r, sizeof r)) return;
+        if (n < kMax) found[n++] = r;
+    };
+    krk_gemm_config plan;
+    auto_config(M, N, K, epilogue, &plan);
+    add(plan);
+    const int nts[] = {1, 2, 4};
+    const int splits[] = {1, 2, 3, 4};
+    if (Mc <= kValuMaxRows)
+        for (int nt : nts)
+            for (int wv : {4, krk::kValuMaxWaves})
+                for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_VALU, 0, nt, 0, wv, sp, 0});
+    for (int nt : nts)
+        for (int pf : {2, 3})
+            for (int kc : {256, 512})
+                for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc});
+    for (int d = 2; d <= 5; ++d)
+        for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});
+    for (int nt : nts)
+        for (int sp : {1, 2, 4}) add(krk_gemm_config{KRK_KERNEL_MFMA, 0, nt, 4, 4, sp, 0});
+    g_err[0] = '\0';  // rejected candidates are not an error of this call
+    for (int i = 0; i < n && i < cap; ++i) out[i] = found[i];
+    return n;
 }
 
 const char* krk_last_error(void) { return g_err; }

@@ -93,6 +93,7 @@ SIGNATURES = {
     "krk_gemm_select_workspace_bytes": (_size, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_gemm_select_plan": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_gemm_select_fused": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_candidates": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig), _int]),
     "krk_last_error": (ctypes.c_char_p, []),
 }
 

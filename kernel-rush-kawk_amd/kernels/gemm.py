@@ -8,9 +8,10 @@ Python surface of libkrk_gemm.so, shaped like the reference's
 * :class:`SkinnyGateUp` — ``f(a, wgu) -> silu(a @ Wg.T) * (a @ Wu.T)`` over the
   concatenated gate-then-up weight (reference ``SkinnyGateUp``,
   engine/kernels/gemm.py:298-329, plus ``swiglu``, engine/kernels/swiglu.py);
-* :func:`pick_matmul` / :func:`pick_gateup` — per-shape callables validated
-  at warm-up against ``torch.nn.functional.linear`` on the same device
-  (reference pickers, engine/kernels/gemm.py:417-498);
+* :func:`pick_matmul` / :func:`pick_gateup` — per-shape callables tuned at
+  warm-up over the library's candidate configurations and validated against
+  ``torch.nn.functional.linear`` on the same device (reference pickers,
+  engine/kernels/gemm.py:417-498; search and cache in :mod:`kernels.tune`);
 * ``norm=(y, w_norm, xout, eps)`` on every call, :func:`pick_normed` and
   :func:`add_rms_norm` — the residual-add + RMSNorm prologue (reference
   engine/kernels/gemm.py:21-51, 501-560 and engine/kernels/add_rmsnorm.py);
@@ -35,7 +36,7 @@ from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "SkinnySelect", "pick_matmul", "pick_gateup", "pick_normed",
-    "add_rms_norm", "plan", "select_plan", "select_fused", "gemm_into", "normed_fused", "_time",
+    "add_rms_norm", "plan", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
 ]
 
 
@@ -325,14 +326,69 @@ def _silu_mul(gu: torch.Tensor) -> torch.Tensor:
     return F.silu(gu[:, :I]) * gu[:, I:]
 
 
-def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = None):
-    """Return ``f(a, w) -> a @ w.T`` for this exact shape (reference
-    engine/kernels/gemm.py:417-458).  The HIP kernel is validated once against
-    ``F.linear`` on the same inputs; with ``log`` its graph-replay time over
-    the ``ws`` rotation is reported in µs and GB/s."""
+def _projection(M: int, N: int, K: int, epilogue: int, device, config: dict | None) -> SkinnyMatmul:
+    if epilogue == EPILOGUE_SILU_MUL:
+        return SkinnyGateUp(M, N // 2, K, device, config)
+    return SkinnyMatmul(M, N, K, device, config)
+
+
+def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_NONE, ws: list | None = None,
+                    log=None, cache=None, norm=None, limit: int | None = None):
+    """Tune the projection ``a @ w.T`` (with ``epilogue``, and with the
+    residual-add + RMSNorm prologue when ``norm=(y, w_norm, eps)``) over the
+    library's candidate configurations on this GPU, timing each as a graph
+    replay over ``ws``.  Returns a :class:`kernels.tune.Result`; the chosen
+    configuration is cached (``cache``, default :func:`kernels.tune.default_cache`)."""
+    from . import tune
+
     M, K = a.shape
     N = w.shape[0]
-    mm = SkinnyMatmul(M, N, K, a.device)
+    rot = ws or [w]
+    cache = tune.default_cache() if cache is None else cache
+    kind = "gateup" if epilogue == EPILOGUE_SILU_MUL else "matmul"
+    if norm is None:
+        ref = _linear_fp32acc(a, w)
+        ref = _silu_mul(ref) if epilogue == EPILOGUE_SILU_MUL else ref
+
+        def build(cfg):
+            mm = _projection(M, N, K, epilogue, a.device, cfg)
+            return lambda w_: mm(a, w_)
+
+        def accept(fn):
+            return tune.max_err_ok(fn(w), ref)
+    else:
+        y, w_norm, eps = norm
+        kind = "normed-" + kind
+        ref_xout, n = _add_rms_norm_ref(a, y, w_norm, eps)
+        ref = _linear_fp32acc(n, w)
+        ref = _silu_mul(ref) if epilogue == EPILOGUE_SILU_MUL else ref
+        xout = torch.empty_like(a)
+
+        def build(cfg):
+            mm = _projection(M, N, K, epilogue, a.device, cfg)
+            return lambda w_: mm(a, w_, norm=(y, w_norm, xout, eps))
+
+        def accept(fn):
+            xout.fill_(0)
+            out = fn(w)
+            if not torch.equal(xout, ref_xout):
+                return False, "xout differs from x + y"
+            return tune.max_err_ok(out, ref)
+    timer = lambda fn, rot_: _time(fn, rotate=rot_)
+    return tune.search(kind, M, N, K, epilogue, a.device, build, accept, timer, rot, log=log, cache=cache, limit=limit)
+
+
+def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = None, tune: bool = True, cache=None):
+    """Return ``f(a, w) -> a @ w.T`` for this exact shape (reference
+    engine/kernels/gemm.py:417-458).  With ``tune`` the configuration is the
+    fastest validated candidate on this GPU (:func:`tune_projection`, within
+    the shared :mod:`kernels.budget`), else the dispatch table's.  The chosen
+    kernel is validated against ``F.linear`` on the same inputs; with ``log``
+    its graph-replay time over the ``ws`` rotation is reported."""
+    M, K = a.shape
+    N = w.shape[0]
+    cfg = tune_projection(a, w, EPILOGUE_NONE, ws, log, cache).config if tune else None
+    mm = SkinnyMatmul(M, N, K, a.device, cfg)
     _validate(mm(a, w), _linear_fp32acc(a, w), f"matmul M={M} N={N} K={K}", log)
     if log:
         ms = _time(lambda w_: mm(a, w_), rotate=ws or [w])
@@ -341,12 +397,14 @@ def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = No
     return mm
 
 
-def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = None):
+def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = None, tune: bool = True, cache=None):
     """Return ``f(a, wgu) -> silu(a @ Wg.T) * (a @ Wu.T)`` (reference
-    engine/kernels/gemm.py:461-498), validated against ``swiglu(F.linear)``."""
+    engine/kernels/gemm.py:461-498), tuned like :func:`pick_matmul` and
+    validated against ``swiglu(F.linear)``."""
     M, K = a.shape
     I = wgu.shape[0] // 2
-    mm = SkinnyGateUp(M, I, K, a.device)
+    cfg = tune_projection(a, wgu, EPILOGUE_SILU_MUL, ws, log, cache).config if tune else None
+    mm = SkinnyGateUp(M, I, K, a.device, cfg)
     _validate(mm(a, wgu), _silu_mul(_linear_fp32acc(a, wgu)), f"gateup M={M} I={I} K={K}", log)
     if log:
         ms = _time(lambda w_: mm(a, w_), rotate=ws or [wgu])
@@ -365,17 +423,21 @@ def _add_rms_norm_ref(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, ep
 
 
 def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, w: torch.Tensor, eps: float,
-                log=None, ws: list | None = None):
+                log=None, ws: list | None = None, tune: bool = True, cache=None):
     """Return ``f(x, y, w_norm, xout, w) -> proj(rms_norm(x + y))`` that also
     writes ``xout = x + y`` (reference engine/kernels/gemm.py:501-560).
-    ``kind`` is "matmul" or "gateup".  Validated once against the torch
+    ``kind`` is "matmul" or "gateup".  Tuned like :func:`pick_matmul` over
+    whole normed calls (the prologue fused or as its own kernel, as each
+    configuration runs it), then validated once against the torch
     composition (xout bit-exact, projection within the reference's
     ``0.02·max|ref| + 1e-3``); with ``log`` the graph-replay time is logged."""
     if kind not in ("matmul", "gateup"):
         raise ValueError(f"kind must be 'matmul' or 'gateup', got {kind!r}")
     M, K = x.shape
     N = w.shape[0]
-    mm = SkinnyGateUp(M, N // 2, K, x.device) if kind == "gateup" else SkinnyMatmul(M, N, K, x.device)
+    epi = EPILOGUE_SILU_MUL if kind == "gateup" else EPILOGUE_NONE
+    cfg = tune_projection(x, w, epi, ws, log, cache, norm=(y, w_norm, eps)).config if tune else None
+    mm = _projection(M, N, K, epi, x.device, cfg)
     fn = lambda x_, y_, wn_, xout_, w_: mm(x_, w_, norm=(y_, wn_, xout_, eps))
     xout = torch.empty_like(x)
     out = fn(x, y, w_norm, xout, w)
@@ -388,7 +450,7 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
     _validate(out, ref, f"normed {kind} M={M} N={N} K={K}", log)
     if log:
         ms = _time(lambda w_: fn(x, y, w_norm, xout, w_), rotate=ws or [w])
-        fused = "fused" if normed_fused(M, N, K, mm.epilogue) else "prologue kernel"
+        fused = "fused" if normed_fused(M, N, K, mm.epilogue, cfg) else "prologue kernel"
         log(f"normed {kind} M={M} N={N} K={K}: krk{mm.resolved_config} ({fused}) {ms * 1000:.1f}us")
     return fn
 

@@ -1,0 +1,220 @@
+"""Warm-up autotuning of the projection GEMM.
+
+The reference picks, at warm-up and per exact shape, the fastest of cuBLAS
+and a list of Triton configurations, each validated against cuBLAS and timed
+as a graph replay over every layer's copy of the weight
+(engine/kernels/gemm.py:378-414 ``_time``, 417-458 ``pick_matmul``, 461-498
+``pick_gateup``, 501-560 ``pick_normed``), within a shared time budget
+(engine/budget.py).  Here:
+
+* the search space is the library's own: ``krk_gemm_candidates`` (C ABI)
+  lists every configuration it accepts for the shape from a fixed grid, the
+  dispatch table's choice first, so the table's plan is always the incumbent;
+* a candidate is accepted under the reference's rule, max error within
+  ``0.02 * max|ref| + 1e-3`` of an fp32-accumulated torch GEMM
+  (gemm.py:441-447), and for normed projections xout bit-equal to x + y
+  (gemm.py:548); a rejected candidate is logged and skipped (it would be a
+  kernel bug: every configuration computes the same function);
+* timing is ``gemm._time`` (graph replay, median of 5, rotating weights);
+* results go to a ``TuneCache`` keyed by GPU architecture, kind and shape,
+  optionally persisted as JSON (``KRK_TUNE_CACHE``), so a serving process
+  tunes once per shape and later processes start from the file.
+
+The winner is always a HIP configuration: torch is not a candidate, so a
+tuned call never leaves the native path.
+
+Command line (from the package directory, GPU required)::
+
+    python -m kernels.tune --M 1,4,16,64 --out tuned.json
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import threading
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib, budget
+
+
+def candidates(M: int, N: int, K: int, epilogue: int = _lib.EPILOGUE_NONE) -> list[dict]:
+    """Every configuration the library accepts for this shape, plan first."""
+    lib = _lib.load()
+    n = lib.krk_gemm_candidates(M, N, K, epilogue, None, 0)
+    _lib.check(min(n, 0))
+    arr = (_lib.GemmConfig * n)()
+    got = lib.krk_gemm_candidates(M, N, K, epilogue, arr, n)
+    _lib.check(min(got, 0))
+    return [c.as_dict() for c in arr[:min(n, got)]]
+
+
+class TuneCache:
+    """Tuned configurations by (architecture, kind, M, N, K); thread-safe.
+    With a path, entries are loaded from and written back to a JSON file
+    (written whole to a temporary file, then renamed)."""
+
+    def __init__(self, path: str | None = None):
+        self.path = path
+        self._lock = threading.Lock()
+        self._d: dict[str, dict] = {}
+        if path and os.path.exists(path):
+            with open(path) as f:
+                self._d = json.load(f)
+
+    @staticmethod
+    def key(device, kind: str, M: int, N: int, K: int) -> str:
+        arch = torch.cuda.get_device_properties(torch.device(device)).gcnArchName.split(":")[0]
+        return f"{arch}/{kind}/M{M}/N{N}/K{K}"
+
+    def get(self, key: str) -> dict | None:
+        with self._lock:
+            e = self._d.get(key)
+            return dict(e["config"]) if e else None
+
+    def put(self, key: str, config: dict, us: float) -> None:
+        with self._lock:
+            self._d[key] = {"config": dict(config), "us": round(us, 2)}
+            if self.path:
+                tmp = f"{self.path}.tmp{os.getpid()}"
+                with open(tmp, "w") as f:
+                    json.dump(self._d, f, indent=1, sort_keys=True)
+                os.replace(tmp, self.path)
+
+    def entries(self) -> dict:
+        with self._lock:
+            return json.loads(json.dumps(self._d))
+
+
+_default_cache: TuneCache | None = None
+_default_lock = threading.Lock()
+
+
+def default_cache() -> TuneCache:
+    """The process-wide cache (file from ``KRK_TUNE_CACHE`` when set)."""
+    global _default_cache
+    with _default_lock:
+        if _default_cache is None:
+            _default_cache = TuneCache(os.environ.get("KRK_TUNE_CACHE") or None)
+        return _default_cache
+
+
+@dataclass
+class Trial:
+    config: dict
+    us: float | None          # None: rejected or failed
+    note: str = ""
+
+
+@dataclass
+class Result:
+    config: dict
+    us: float
+    plan_us: float | None     # the dispatch table's configuration, when measured
+    cached: bool = False
+    trials: list = field(default_factory=list)
+
+
+def max_err_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
+    """The reference's acceptance rule (engine/kernels/gemm.py:441-447)."""
+    out, ref = out.float(), ref.float()
+    err = (out - ref).abs().max().item()
+    tol = 0.02 * ref.abs().max().item() + 1e-3
+    return err <= tol, f"err {err:.4g} vs tol {tol:.4g}"
+
+
+def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, accept, timer, rot: list,
+           log=None, cache: TuneCache | None = None, limit: int | None = None) -> Result:
+    """Tune one shape.
+
+    build(cfg) -> fn(w) runs the candidate on weight w and returns its output;
+    accept(fn) -> (ok, text) validates one call; timer(fn, rot) -> ms per call.
+    The plan (first candidate) is always measured; the rest while the budget
+    lasts (at most ``limit`` candidates in all when given)."""
+    key = TuneCache.key(device, kind, M, N, K) if cache is not None else None
+    if cache is not None:
+        hit = cache.get(key)
+        if hit is not None:
+            if log:
+                log(f"tune {kind} M={M} N={N} K={K}: cached krk{hit}")
+            return Result(hit, float("nan"), None, cached=True)
+    cands = candidates(M, N, K, epilogue)
+    if limit is not None:
+        cands = cands[:max(1, limit)]
+    trials: list[Trial] = []
+    best: tuple[float, dict] | None = None
+    plan_us = None
+    for i, cfg in enumerate(cands):
+        if i > 0 and budget.expired():
+            break
+        try:
+            fn = build(cfg)
+            ok, why = accept(fn)
+            if not ok:
+                trials.append(Trial(cfg, None, "rejected: " + why))
+                if log:
+                    log(f"tune {kind} M={M} N={N} K={K}: krk{cfg} rejected ({why})")
+                continue
+            us = timer(fn, rot) * 1000.0
+        except (ValueError, RuntimeError) as exc:  # a configuration this shape cannot use
+            trials.append(Trial(cfg, None, f"failed: {exc}"))
+            continue
+        trials.append(Trial(cfg, us))
+        if i == 0:
+            plan_us = us
+        if best is None or us < best[0]:
+            best = (us, cfg)
+    if best is None:
+        raise RuntimeError(f"tune {kind} M={M} N={N} K={K}: no candidate passed validation")
+    res = Result(best[1], best[0], plan_us, trials=trials)
+    if cache is not None:
+        cache.put(key, res.config, res.us)
+    if log:
+        gain = f", plan {plan_us:.1f}us" if plan_us is not None else ""
+        log(f"tune {kind} M={M} N={N} K={K}: krk{res.config} {res.us:.1f}us over {len(trials)} candidates{gain}")
+    return res
+
+
+def main(argv=None) -> int:
+    import argparse
+
+    from . import gemm as G
+
+    p = argparse.ArgumentParser(description="Tune the Qwen3-4B decode projections on this GPU.")
+    p.add_argument("--M", default="1,2,4,8,16,32,64", help="comma-separated row counts")
+    p.add_argument("--shapes", default="qkv,o,gate_up,down,lm_head")
+    p.add_argument("--copies", type=int, default=8, help="distinct weight copies rotated while timing")
+    p.add_argument("--out", default=None, help="JSON cache file to write")
+    p.add_argument("--seconds", type=float, default=0.0, help="budget per shape (0: no limit)")
+    args = p.parse_args(argv)
+    shapes = {"qkv": (2560, 6144, 0), "o": (4096, 2560, 0), "gate_up": (2560, 19456, 1),
+              "down": (9728, 2560, 0), "lm_head": (2560, 151936, 0)}
+    dev = torch.device("cuda:0")
+    cache = TuneCache(args.out)
+    g = torch.Generator(device=dev).manual_seed(0)
+    rows = []
+    for name in args.shapes.split(","):
+        K, N, epi = shapes[name]
+        copies = 2 if name == "lm_head" else args.copies
+        ws = [torch.randn((N, K), device=dev, generator=g).mul_(0.02).to(torch.bfloat16) for _ in range(copies)]
+        for M in map(int, args.M.split(",")):
+            a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+            if args.seconds > 0:
+                budget.start(args.seconds)
+            else:
+                budget.clear()
+            r = G.tune_projection(a, ws[0], epi, ws=ws, cache=cache)
+            rows.append((name, M, r.plan_us, r.us, r.config))
+            print(f"{name:8s} M={M:3d} plan {r.plan_us:8.2f} us  tuned {r.us:8.2f} us  krk{r.config}", flush=True)
+            del a
+        del ws
+        torch.cuda.empty_cache()
+    budget.clear()
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

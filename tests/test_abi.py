@@ -378,3 +378,42 @@ def test_select_plan_and_workspace(lib):
     assert lib.krk_gemm_select_plan(1, N, K, 0, ctypes.byref(c)) == _lib.KRK_ERR_INVALID
     bad = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_MFMA_LDS, k_chunk=384))
     assert lib.krk_gemm_select_workspace_bytes(32, N, K, 1, ctypes.byref(bad)) == 0
+
+
+# ------------------------------------------------------------------ tuner search space
+
+@pytest.mark.parametrize("M", [1, 4, 8, 9, 32, 64, 100])
+def test_candidates_search_space(lib, M):
+    """krk_gemm_candidates: the plan first, then distinct configurations the
+    library accepts (resolved: no field left at 0), VALU only up to 8 rows;
+    a short array receives the first cap entries."""
+    for N, K, epi in QWEN.values():
+        n = lib.krk_gemm_candidates(M, N, K, epi, None, 0)
+        assert n > 8, (M, N, K, n)
+        arr = (GemmConfig * n)()
+        assert lib.krk_gemm_candidates(M, N, K, epi, arr, n) == n
+        cfgs = [c.as_dict() for c in arr]
+        plan = GemmConfig()
+        assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(plan)) == 0
+        assert cfgs[0] == plan.as_dict()
+        assert len({tuple(sorted(c.items())) for c in cfgs}) == n
+        kinds = {c["kernel"] for c in cfgs}
+        assert (_lib.KERNEL_VALU in kinds) == (min(M, 64) <= 8)
+        assert {_lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM} <= kinds
+        for c in cfgs:
+            assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_VALU, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM)
+            assert all(c[f] > 0 for f in ("m_tiles", "n_tiles", "unroll", "waves", "splits")), c
+            if c["kernel"] == _lib.KERNEL_MFMA_LDS:
+                assert c["k_chunk"] in (256, 512)
+            if epi == SILU and c["kernel"] != _lib.KERNEL_STREAM:
+                assert c["n_tiles"] % 2 == 0, c
+            # Each one is accepted again as an explicit configuration.
+            cfg = GemmConfig.from_dict(c)
+            if c["splits"] > 1:
+                assert lib.krk_gemm_config_workspace_bytes(M, N, K, epi, ctypes.byref(cfg)) > 0, c
+        short = (GemmConfig * 3)()
+        assert lib.krk_gemm_candidates(M, N, K, epi, short, 3) == n
+        assert [c.as_dict() for c in short] == cfgs[:3]
+    assert lib.krk_gemm_candidates(1, 64, 12, NONE, None, 0) == _lib.KRK_ERR_INVALID
+    assert lib.krk_gemm_candidates(1, 64, 64, NONE, None, -1) == _lib.KRK_ERR_INVALID
+    assert lib.krk_gemm_candidates(1, 64, 64, NONE, None, 4) == _lib.KRK_ERR_INVALID

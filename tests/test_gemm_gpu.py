@@ -498,6 +498,63 @@ def test_pickers_return_validated_callables(device):
     assert any("us" in l for l in logs)
 
 
+# ------------------------------------------------------------------ warm-up tuner
+
+_TUNE_SHAPES = {"qkv": (2560, 6144, NONE), "o": (4096, 2560, NONE), "gate_up": (2560, 19456, SILU),
+                "down": (9728, 2560, NONE), "lm_head": (2560, 151936, NONE)}
+
+
+@pytest.mark.parametrize("shape,M", [("qkv", 8), ("gate_up", 4), ("down", 32), ("o", 64), ("lm_head", 1)])
+def test_tune_validates_every_candidate(device, shape, M):
+    """The tuner runs every candidate configuration at a real shape: each
+    must pass the reference's acceptance rule (a rejection is a kernel bug),
+    the winner is no slower than the table's plan, and a second tuning of
+    the shape comes from the cache."""
+    from kernels import tune as T
+    K, N, epi = _TUNE_SHAPES[shape]
+    a = R.randn_bf16((M, K), 9600 + M).to(device)
+    ws = [R.randn_bf16((N, K), 9601 + i, 0.02).to(device) for i in range(2)]
+    cache = T.TuneCache()
+    say("tune", shape, M, len(T.candidates(M, N, K, epi)), "candidates")
+    r = G.tune_projection(a, ws[0], epi, ws=ws, cache=cache)
+    bad = [(t.config, t.note) for t in r.trials if t.us is None]
+    assert not bad, f"candidates rejected or failed: {bad[:3]}"
+    assert len(r.trials) == len(T.candidates(M, N, K, epi))
+    assert r.trials[0].config == G.plan(M, N, K, epi) and r.plan_us is not None
+    assert r.us <= r.plan_us
+    again = G.tune_projection(a, ws[0], epi, ws=ws, cache=cache)
+    assert again.cached and again.config == r.config
+    mm = G.SkinnyGateUp(M, N // 2, K, device, r.config) if epi == SILU else G.SkinnyMatmul(M, N, K, device, r.config)
+    ref = R.gateup_bf16(a.cpu(), ws[1].cpu()) if epi == SILU else R.linear_bf16(a.cpu(), ws[1].cpu())
+    assert_parity(mm(a, ws[1]).cpu(), ref, f"tuned {shape} M={M}")
+
+
+def test_tune_budget_cache_file_and_normed(device, tmp_path):
+    """An expired budget measures only the plan; results persist to the JSON
+    cache file and load in a new cache; normed tuning validates xout too."""
+    from kernels import budget, tune as T
+    M, K, N = 2, 2560, 6144
+    a = R.randn_bf16((M, K), 9700).to(device)
+    w = R.randn_bf16((N, K), 9701, 0.02).to(device)
+    path = str(tmp_path / "tuned.json")
+    budget.start(0.0)
+    try:
+        r = G.tune_projection(a, w, NONE, cache=T.TuneCache(path))
+    finally:
+        budget.clear()
+    assert len(r.trials) == 1 and r.config == G.plan(M, N, K, NONE)
+    loaded = T.TuneCache(path)
+    assert loaded.get(T.TuneCache.key(device, "matmul", M, N, K)) == r.config
+    x, y, wn = (t.to(device) for t in _norm_inputs(M, K, 9702))
+    rn = G.tune_projection(x, w, NONE, cache=T.TuneCache(), norm=(y, wn, EPS), limit=12)
+    assert len(rn.trials) == 12 and all(t.us is not None for t in rn.trials), [t.note for t in rn.trials]
+    f = G.pick_normed("matmul", x, y, wn, w, EPS, cache=T.TuneCache(), tune=True)
+    xo = torch.empty_like(x)
+    out = f(x, y, wn, xo, w)
+    torch.cuda.synchronize()
+    _check_normed(x.cpu(), y.cpu(), wn.cpu(), w.cpu(), NONE, xo.cpu(), out.cpu(), "tuned pick_normed")
+
+
 # ------------------------------------------------------------------ normed projections (RMSNorm prologue)
 
 EPS = 1e-6
