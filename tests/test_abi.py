@@ -417,3 +417,17 @@ def test_candidates_search_space(lib, M):
     assert lib.krk_gemm_candidates(1, 64, 12, NONE, None, 0) == _lib.KRK_ERR_INVALID
     assert lib.krk_gemm_candidates(1, 64, 64, NONE, None, -1) == _lib.KRK_ERR_INVALID
     assert lib.krk_gemm_candidates(1, 64, 64, NONE, None, 4) == _lib.KRK_ERR_INVALID
+
+
+def test_package_loads_under_another_name():
+    """The engine's own ``kernels`` package takes that name: krk_loader
+    imports this one as a separate package, sharing the one HIP library."""
+    import krk_loader
+    import kernels
+
+    krk = krk_loader.load("krk_alias_for_test")
+    assert krk is not kernels and krk.gemm is not kernels.gemm
+    assert callable(krk.step.decode_matmuls) and callable(krk.gemm.SkinnyMatmul)
+    assert krk._lib.LIB_PATH == kernels._lib.LIB_PATH
+    assert krk_loader.load("krk_alias_for_test") is krk
+    assert krk.tune.candidates(1, 6144, 2560)[0] == kernels.gemm.plan(1, 6144, 2560)
