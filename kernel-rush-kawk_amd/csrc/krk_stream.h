@@ -116,7 +116,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const int ch = b * CB + row;
                 wr = ch < Nout ? ch : Nout - 1;
             }
-            dma_row(w + (int64_t)wr * ldw + kc, slot + row * kStreamPitch);
+            dma_row_stream(w + (int64_t)wr * ldw + kc, slot + row * kStreamPitch);
         }
     };
     // x for the workgroup's K range, loaded once.  Whole 1 KB row pieces (wave

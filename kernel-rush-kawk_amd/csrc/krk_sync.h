@@ -55,5 +55,13 @@ __device__ __forceinline__ void bare_barrier() {
 __device__ __forceinline__ void dma_row(const uint16_t* src_lane, unsigned char* dst_row) {
     __builtin_amdgcn_global_load_lds((gbl_void_t*)src_lane, (lds_void_t*)dst_row, 16, 0, 0);
 }
+// The same for data read once (weight rows): the nontemporal policy (nt)
+// keeps the stream from evicting what is reused from L2, such as x, which
+// every workgroup reads (measured: the stream kernel's x preload 3.65 ->
+// 3.4 us at gate_up M = 32).
+__device__ __forceinline__ void dma_row_stream(const uint16_t* src_lane, unsigned char* dst_row) {
+    constexpr int kNontemporal = 2;  // cache-policy bit NT of the gfx950 global load
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)src_lane, (lds_void_t*)dst_row, 16, 0, kNontemporal);
+}
 
 }  // namespace krk
