@@ -12,6 +12,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <utility>
 
 #include "krk_gemm.h"
@@ -396,6 +397,21 @@ int hip_status(hipError_t e, const char* what) {
     return fail(KRK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Raise a kernel's dynamic-LDS limit to `bytes` on the calling thread's
+// current device, once per device and kernel (the attribute is set in the
+// device's context, so a process that drives several GPUs needs it on each).
+// `done` is the kernel's own set of devices already configured.
+hipError_t ensure_lds_limit(const void* fn, int bytes, std::atomic<uint64_t>& done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+    return e;
+}
+
 template <int MT, int NT, int U, bool SILU>
 int launch_mfma(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream) {
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
@@ -446,8 +462,8 @@ int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::S
         const size_t shm = krk::mfma_lds_bytes(MT, NT, KC, SEL);
         // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once
         // per instantiation (a function attribute, not a stream operation).
-        static const hipError_t attr =
-            shm > 65536 ? hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) : hipSuccess;
+        static std::atomic<uint64_t> done{0};
+        const hipError_t attr = shm > 65536 ? ensure_lds_limit(fn, (int)shm, done) : hipSuccess;
         if (attr != hipSuccess) return hip_status(attr, "mfma_lds_kernel LDS attribute");
         void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
                         (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr,
@@ -506,7 +522,8 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     }
     if (shm > kLdsMax || (a.splits == 1 && obcap < 1))
         return fail(KRK_ERR_UNSUPPORTED, "STREAM depth %d leaves no LDS for the output buffer", depth);
-    static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    static std::atomic<uint64_t> done{0};
+    const hipError_t attr = ensure_lds_limit(fn, (int)kLdsMax, done);
     if (attr != hipSuccess) return hip_status(attr, "stream_gemm_kernel LDS attribute");
     const int groups = G * a.splits;
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
@@ -564,12 +581,9 @@ int launch_valu(const LaunchArgs& a, int nblocks, int waves, hipStream_t stream,
                            : reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM, SEL>);
     const size_t shm = NORM ? krk::valu_norm_lds_bytes(MX, nb) : krk::valu_lds_bytes(MX, cdiv(nb, a.splits));
     if (NORM || MX >= krk::kValuLdsMinRows) {
-        static const hipError_t attr[2] = {
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, false, NORM, SEL>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax),
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&krk::valu_gemm_kernel<MX, R, D, SILU, true, NORM, SEL>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax)};
-        if (attr[exact] != hipSuccess) return hip_status(attr[exact], "valu_gemm_kernel LDS attribute");
+        static std::atomic<uint64_t> done[2] = {{0}, {0}};
+        const hipError_t attr = ensure_lds_limit(fn, (int)kLdsMax, done[exact]);
+        if (attr != hipSuccess) return hip_status(attr, "valu_gemm_kernel LDS attribute");
     }
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy, (void*)&a.M,
                     (void*)&a.N, (void*)&a.K,   (void*)&per, (void*)&rem, (void*)&a.part, (void*)&a.ctr, (void*)&na, (void*)&sa};

@@ -214,6 +214,29 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
             for (int r = 0; r < R; ++r) wv[d][r] = load_row16_nt(wrow[r], 2u * koff(b + d));
     };
 
+    // After this wave's LDS DMAs: issue the W loads of the first chunk and
+    // wait until the DMAs have landed.  vmcnt retires in order, so with the
+    // D·R W loads issued strictly after the DMAs, vmcnt <= D·R means every
+    // DMA is done while the W loads stay in flight.  That holds when every
+    // load stays between the scheduling barriers: in EXACT variants each
+    // loaded block is used unconditionally, and the compiler keeps them
+    // there (the library's disassembly is checked by a test); in the other
+    // variants a load used under a condition can be sunk below the wait
+    // (observed), so they drain vmcnt completely.
+    auto issue_first_chunk = [&](int b) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        issue(b);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if constexpr (EXACT) {
+            vm_wait<D * R>();
+        } else {
+            vm_wait<0>();
+        }
+    };
+
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
@@ -285,9 +308,9 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
             const uint16_t* src = (isd ? drow[m] : xrow[m]) + kfull(bb);
             dma_row(src, (isd ? ds : xs) + (size_t)jj * (kValuBlock * 2));
         }
-        issue(b0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        vm_wait<0>();
+        // The first W loads go out behind the DMAs, and (EXACT) only the DMAs
+        // are waited for: the statistics below overlap the weight stream.
+        issue_first_chunk(b0);
         bare_barrier();
         // Sums of squares of s = bf16(x + d) per row; s replaces x in LDS.
         const bool write_xout = blockIdx.x == 0 && blockIdx.y == 0;
@@ -342,9 +365,9 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     } else if constexpr (XLDS) {
         // x[0:MX, b0*512 : b1*512) into LDS as [m][block][512], one 1 KB DMA
         // per (row, block), spread over the waves; the first W loads go out
-        // behind them.  The barrier publishes x after a full vmcnt drain: the
-        // compiler may move plain W loads across the barrier, so a partial
-        // count could let a DMA still be in flight.
+        // behind them.  The barrier publishes x once the DMAs have landed
+        // (issue_first_chunk), and in EXACT variants block 0 is consumed as
+        // soon as its own W rows land.
         const int nblk = b1 - b0;
         int m = 0, bi = wave;
         while (bi >= nblk) bi -= nblk, ++m;
@@ -353,9 +376,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
             bi += waves;
             while (bi >= nblk) bi -= nblk, ++m;
         }
-        issue(b0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        vm_wait<0>();
+        issue_first_chunk(b0);
         bare_barrier();
         consume(b0);
         b += D;
