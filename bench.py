@@ -103,6 +103,9 @@ def main() -> int:
     ap.add_argument("--no-torch", action="store_true", help="skip the torch-GPU comparison timings")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample length")
+    ap.add_argument("--profile-shape", choices=sorted(SHAPES), default=None,
+                    help="only replay one projection at --M over its distinct weights (graph of 36 launches, 8 for "
+                         "lm_head, 4 replays) and a 256 MiB device copy: the counter workload of profiles/")
     ap.add_argument("--profile-dominant", action="store_true",
                     help="only replay the dominant kernel (gate_up at --M over 36 layer weights, 3 graph replays) "
                          "and a 256 MiB device copy: the workload the committed rocprofv3 --pmc summaries measure")
@@ -128,6 +131,8 @@ def main() -> int:
 
     if args.profile_dominant:
         return profile_dominant(torch, G, dev, args.M)
+    if args.profile_shape:
+        return profile_shape(torch, G, dev, args.profile_shape, args.M)
 
     # ------------------------------------------------------------ weights
     t0 = time.time()
@@ -451,27 +456,40 @@ def measured_traffic(name: str, M: int, config: dict):
     return rec.get("traffic_bytes_per_launch")
 
 
-def profile_dominant(torch, G, dev, M: int) -> int:
-    """Workload for the counter runs: 3 replays of a graph of 36 gate_up
-    launches (distinct layer weights, as in the sweep), then 4 copies of a
-    256 MiB buffer for the counters' byte calibration."""
-    K, Nw, _ = SHAPES["gate_up"]
-    ws = [randn_bf16(torch, (Nw, K), seed_for(4, l, "gate_up"), 0.02, dev) for l in range(LAYERS)]
+def profile_shape(torch, G, dev, name: str, M: int) -> int:
+    """Workload for the counter runs: replays of a graph of launches of one
+    projection over distinct weights (the 36 layer weights of the sweep; for
+    lm_head 2 copies, 8 launches), then 4 copies of a 256 MiB buffer for the
+    counters' byte calibration.  Prints the configuration and the event-timed
+    µs per launch of the graph (median of 3 replays after 10 warm-up ones)."""
+    K, Nw, silu = SHAPES[name]
+    if name == "lm_head":
+        ws = [randn_bf16(torch, (Nw, K), seed_for(4, 99, "lm_head") + i, 0.02, dev) for i in range(2)] * 4
+    else:
+        ws = [randn_bf16(torch, (Nw, K), seed_for(4, l, name), 0.02, dev) for l in range(LAYERS)]
     x = randn_bf16(torch, (M, K), seed_for(4, 0, "x") + K, 1.0, dev)
-    op = G.SkinnyGateUp(M, Nw // 2, K, dev)
-    out = torch.empty((M, Nw // 2), dtype=torch.bfloat16, device=dev)
+    op = G.SkinnyGateUp(M, Nw // 2, K, dev) if silu else G.SkinnyMatmul(M, Nw, K, dev)
+    out = torch.empty((M, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
     calls = [(lambda w=w: op.run(x, w, out)) for w in ws]
     _, g = graph_time_ms(torch, calls, reps=1)
-    for _ in range(3):
+    for _ in range(8):  # bring the clocks up before the timed replays
         g.replay()
+    ms, _ = graph_time_ms(torch, calls, reps=3)
     a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
     for _ in range(4):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"profile": "dominant", "shape": "gate_up", "M": M, "config": op.resolved_config,
+    print(json.dumps({"profile": name, "shape": name, "M": M, "config": op.resolved_config,
+                      "kernel": KERNEL_NAMES[op.resolved_config["kernel"]], "us_per_launch": round(ms * 1000, 3),
+                      "algorithmic_bytes": algo_bytes(name, M), "launches": len(calls) * 14,
                       "copy_bytes": 256 << 20, "copies": 4}), flush=True)
     return 0
+
+
+def profile_dominant(torch, G, dev, M: int) -> int:
+    """The dominant kernel's counter workload (gate_up at --M)."""
+    return profile_shape(torch, G, dev, "gate_up", M)
 
 
 def cpu_baseline(torch, layer0, lm0, x, M, seconds):
