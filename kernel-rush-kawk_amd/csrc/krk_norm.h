@@ -89,13 +89,16 @@ add_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t ldx, NormArgs a,
     uint16_t* xo = a.xout + (int64_t)m * a.ldxo;
     uint16_t* nr = n + (int64_t)m * ldn;
 
-    u32x4 s[kNormMaxVec];
+    // The gain is loaded with x and d, so the normalisation after the
+    // reduction needs no further memory round trip.
+    u32x4 s[kNormMaxVec], g[kNormMaxVec];
     float ss = 0.0f;
 #pragma unroll
     for (int v = 0; v < kNormMaxVec; ++v) {
         const int k = 8 * (t + kNormThreads * v);
         if (k < K) {
             s[v] = add_bf16x8(*reinterpret_cast<const u32x4*>(xr + k), *reinterpret_cast<const u32x4*>(dr + k));
+            g[v] = *reinterpret_cast<const u32x4*>(a.wn + k);
             *reinterpret_cast<u32x4*>(xo + k) = s[v];
             ss = sumsq_bf16x8(s[v], ss);
         }
@@ -112,8 +115,7 @@ add_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t ldx, NormArgs a,
 #pragma unroll
     for (int v = 0; v < kNormMaxVec; ++v) {
         const int k = 8 * (t + kNormThreads * v);
-        if (k < K)
-            *reinterpret_cast<u32x4*>(nr + k) = normalize_bf16x8(s[v], rstd, *reinterpret_cast<const u32x4*>(a.wn + k));
+        if (k < K) *reinterpret_cast<u32x4*>(nr + k) = normalize_bf16x8(s[v], rstd, g[v]);
     }
 }
 

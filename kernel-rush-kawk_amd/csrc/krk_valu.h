@@ -44,9 +44,10 @@ __host__ __device__ constexpr size_t valu_lds_bytes(int MX, int blocks) {
     return MX < kValuLdsMinRows ? 0 : (size_t)MX * blocks * kValuBlock * sizeof(uint16_t);
 }
 // With the fused RMSNorm prologue: x and the branch rows of the whole K
-// (nb blocks), then the per-wave partial sums of squares.
+// (nb blocks), the RMSNorm gain (nb blocks), then the per-wave partial sums
+// of squares.
 __host__ __device__ constexpr size_t valu_norm_lds_bytes(int MX, int nb) {
-    return (size_t)2 * MX * nb * kValuBlock * sizeof(uint16_t) + (size_t)MX * kValuMaxWaves * sizeof(float);
+    return (size_t)(2 * MX + 1) * nb * kValuBlock * sizeof(uint16_t) + (size_t)MX * kValuMaxWaves * sizeof(float);
 }
 
 __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
@@ -290,9 +291,12 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     int b = b0;
     if constexpr (NORM) {
         // x and d rows of the whole K into LDS as [m][block][512] (x, then d),
-        // one 1 KB DMA per (row, block); then the first W loads.
+        // and the gain as [block][512], one 1 KB DMA per (row, block); then
+        // the first W loads.  (A global load of the gain after the W loads
+        // would wait behind them: vmcnt retires in order.)
         unsigned char* const ds = xs + (size_t)MX * nb * kValuBlock * 2;
-        float* const red = reinterpret_cast<float*>(ds + (size_t)MX * nb * kValuBlock * 2);
+        unsigned char* const gs = ds + (size_t)MX * nb * kValuBlock * 2;
+        float* const red = reinterpret_cast<float*>(gs + (size_t)nb * kValuBlock * 2);
         const uint16_t* drow[MX];
 #pragma unroll
         for (int m = 0; m < MX; ++m) drow[m] = na.d + (int64_t)(m < M ? m : M - 1) * na.ldd;
@@ -308,6 +312,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
             const uint16_t* src = (isd ? drow[m] : xrow[m]) + kfull(bb);
             dma_row(src, (isd ? ds : xs) + (size_t)jj * (kValuBlock * 2));
         }
+        for (int bb = wave; bb < nb; bb += waves) dma_row(na.wn + kfull(bb), gs + (size_t)bb * (kValuBlock * 2));
         // The first W loads go out behind the DMAs, and (EXACT) only the DMAs
         // are waited for: the statistics below overlap the weight stream.
         issue_first_chunk(b0);
@@ -350,7 +355,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
         for (int e = threadIdx.x; e < (b1 - b0) * 64; e += blockDim.x) {
             const uint32_t k = (uint32_t)b0 * kValuBlock + 8u * (uint32_t)e;
             if (k < (uint32_t)K) {
-                const u32x4 g = *reinterpret_cast<const u32x4*>(na.wn + k);
+                const u32x4 g = *reinterpret_cast<const u32x4*>(gs + (size_t)k * 2);
 #pragma unroll
                 for (int m = 0; m < MX; ++m) {
                     unsigned char* px = xs + ((size_t)m * nb * kValuBlock + k) * 2;
