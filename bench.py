@@ -247,6 +247,51 @@ def main() -> int:
                 log(f"M={Mt:3d} {name:8s} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s {row['pct_peak']:5.1f}%"
                     + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
 
+    # ------------------------------------------------------------ one GPU's 8-way tensor-parallel shard
+    # The per-GPU shapes of an 8-GPU deployment (QKV, gate_up and lm_head
+    # column-parallel, o and down row-parallel), at their real sizes: the
+    # dispatch rule's plan, the warm-up tuner's choice (3 s budget per shape),
+    # and torch, each over enough distinct weight copies to exceed the
+    # 256 MB Infinity Cache.
+    shards = []
+    if not args.no_table:
+        from kernels import budget as B
+        from kernels import tune as T
+
+        tp8 = {"qkv": (2560, 768, False), "gate_up": (2560, 2 * 1216, True), "o": (512, 2560, False),
+               "down": (1216, 2560, False), "lm_head": (2560, 18992, False)}
+        for name, (K, Nw, silu) in tp8.items():
+            copies = min(128, -(-(300 << 20) // (Nw * K * 2)))
+            wsh = [randn_bf16(torch, (Nw, K), 7000 + 131 * i + Nw, 0.02, dev) for i in range(copies)]
+            for Mt in (1, 32):
+                xt = randn_bf16(torch, (Mt, K), 7001 + Mt + K, 1.0, dev)
+                epi = G.EPILOGUE_SILU_MUL if silu else G.EPILOGUE_NONE
+                op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
+                ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
+                calls = [(lambda w=w: op.run(xt, w, ot)) for w in wsh]
+                ms, _ = graph_time_ms(torch, calls)
+                B.start(3.0)
+                try:
+                    tuned = G.tune_projection(xt, wsh[0], epi, ws=wsh, cache=T.TuneCache())
+                finally:
+                    B.clear()
+                nout = Nw // 2 if silu else Nw
+                bytes_ = 2 * (Nw * K + Mt * K + Mt * nout)
+                row = {"shard": name, "N_w": Nw, "K": K, "M": Mt, "us": round(ms * 1000, 2),
+                       "GBps": round(bytes_ / (ms * 1e-3) / 1e9, 1), "config": op.resolved_config,
+                       "tuned_us": round(tuned.us, 2), "tuned_config": tuned.config, "candidates_timed": len(tuned.trials)}
+                if not args.no_torch:
+                    if silu:
+                        tc = [(lambda w=w: (lambda r: F.silu(r[:, :Nw // 2]) * r[:, Nw // 2:])(F.linear(xt, w))) for w in wsh]
+                    else:
+                        tc = [(lambda w=w: F.linear(xt, w)) for w in wsh]
+                    tms, _ = graph_time_ms(torch, tc)
+                    row["torch_gpu_us"] = round(tms * 1000, 2)
+                shards.append(row)
+                log(f"tp8 shard {name:8s} M={Mt:3d} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s   tuned {row['tuned_us']:8.2f} us"
+                    + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
+            del wsh
+
     # ------------------------------------------------------------ normed projections
     # The qkv, gate_up and lm_head calls of a decode step take rms_norm(x + y)
     # as input (the reference's pick_normed contract).  Three ways of running
@@ -434,6 +479,7 @@ def main() -> int:
         "normed": normed,
         "select": select,
         "decode_step": step_rows,
+        "tp8_shard": shards,
     }
     print(json.dumps(result), flush=True)
     return 0

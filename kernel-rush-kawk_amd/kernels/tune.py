@@ -26,6 +26,7 @@ tuned call never leaves the native path.
 Command line (from the package directory, GPU required)::
 
     python -m kernels.tune --M 1,4,16,64 --out tuned.json
+    python -m kernels.tune --tp 8 --out tuned_tp8.json    # one GPU's 8-way shard
 """
 
 from __future__ import annotations
@@ -189,16 +190,23 @@ def main(argv=None) -> int:
     p.add_argument("--copies", type=int, default=8, help="distinct weight copies rotated while timing")
     p.add_argument("--out", default=None, help="JSON cache file to write")
     p.add_argument("--seconds", type=float, default=0.0, help="budget per shape (0: no limit)")
+    p.add_argument("--tp", type=int, default=1,
+                   help="tune one GPU's shard under this tensor-parallel degree (N of qkv, gate_up and lm_head, "
+                        "K of o and down divided by it)")
     args = p.parse_args(argv)
-    shapes = {"qkv": (2560, 6144, 0), "o": (4096, 2560, 0), "gate_up": (2560, 19456, 1),
-              "down": (9728, 2560, 0), "lm_head": (2560, 151936, 0)}
+    t = args.tp
+    if t < 1 or 6144 % t or 9728 % t or 4096 % t or 151936 % t:
+        p.error(f"--tp {t} does not divide the Qwen3-4B shapes")
+    shapes = {"qkv": (2560, 6144 // t, 0), "o": (4096 // t, 2560, 0), "gate_up": (2560, 2 * (9728 // t), 1),
+              "down": (9728 // t, 2560, 0), "lm_head": (2560, 151936 // t, 0)}
     dev = torch.device("cuda:0")
     cache = TuneCache(args.out)
     g = torch.Generator(device=dev).manual_seed(0)
     rows = []
     for name in args.shapes.split(","):
         K, N, epi = shapes[name]
-        copies = 2 if name == "lm_head" else args.copies
+        copies = max(2, min(args.copies * t, -(-(300 << 20) // (N * K * 2)))) if t > 1 else \
+            (2 if name == "lm_head" else args.copies)
         ws = [torch.randn((N, K), device=dev, generator=g).mul_(0.02).to(torch.bfloat16) for _ in range(copies)]
         for M in map(int, args.M.split(",")):
             a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)

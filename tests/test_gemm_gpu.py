@@ -206,6 +206,29 @@ def test_ragged_gateup(device, M, I, K):
     check_gateup(x, w, f"ragged gateup M={M} I={I} K={K}")
 
 
+# One GPU's shard of each projection under 8-way tensor parallelism (the
+# narrow-N / short-K shapes a multi-GPU deployment would run per GPU): QKV and
+# lm_head column-parallel, gate_up with gate and up rows sharded together, o
+# and down row-parallel.
+TP8_SHARDS = {"qkv": (768, 2560, NONE), "gate_up": (2 * 1216, 2560, SILU), "o": (2560, 512, NONE),
+              "down": (2560, 1216, NONE), "lm_head": (18992, 2560, NONE)}
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 13, 16, 24, 32, 48, 64])
+@pytest.mark.parametrize("shard", sorted(TP8_SHARDS))
+def test_tp8_shard_shapes(device, shard, M):
+    N, K, epi = TP8_SHARDS[shard]
+    x = R.randn_bf16((M, K), 7800 + M + K)
+    w = R.randn_bf16((N, K), 7900 + N, 0.02)
+    say("tp8 shard", shard, M, G.plan(M, N, K, epi))
+    if epi == SILU:
+        check_gateup(x, w, f"tp8 {shard} M={M}")
+    elif shard == "lm_head":
+        _lm_argmax_check(x, w, f"tp8 lm_head M={M}", device)
+    else:
+        check_linear(x, w, f"tp8 {shard} M={M}")
+
+
 def test_strided_operands(device):
     """x a column slice of a wider buffer (ldx > K), y written into a wider buffer."""
     K, N, M = 2560, 300, 5
