@@ -107,7 +107,8 @@ const TableEntry kTable[] = {
     {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
     {2560, 4096, KRK_EPILOGUE_NONE, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
     {2560, 4096, KRK_EPILOGUE_NONE, 25, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
@@ -126,8 +127,7 @@ const TableEntry kTable[] = {
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 5, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 33, 48, kcfg(KRK_KERNEL_STREAM, 1, 3, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
 
@@ -1240,12 +1240,15 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
         for (int nt : nts)
             for (int wv : {4, krk::kValuMaxWaves})
                 for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_VALU, 0, nt, 0, wv, sp, 0});
+    // More splits for the weight-streaming MFMA kernels: at M >= 16 they cut
+    // each workgroup's share of x, the bound of narrow-N, long-K shapes.
+    const int wide_splits[] = {1, 2, 3, 4, 6, 8};
     for (int nt : nts)
         for (int pf : {2, 3})
             for (int kc : {256, 512})
-                for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc});
+                for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc});
     for (int d = 2; d <= 5; ++d)
-        for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});
+        for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});
     for (int nt : nts)
         for (int sp : {1, 2, 4}) add(krk_gemm_config{KRK_KERNEL_MFMA, 0, nt, 4, 4, sp, 0});
     g_err[0] = '\0';  // rejected candidates are not an error of this call

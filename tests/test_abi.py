@@ -338,13 +338,14 @@ def test_select_argument_errors(lib, kw, code, msg):
 
 def test_select_plan_and_workspace(lib):
     """The projection plan is the plain table's; argmax fuses into the VALU
-    (M <= 4) and LDS-staged MFMA (M <= 16) plans, never into the stream
-    kernel (M >= 17) or a top-k.  Workspace: the row counters, then the
-    per-workgroup keys (fused) or a logits buffer, then the per-chunk lists."""
+    (M <= 4) plans and LDS-staged MFMA configurations, never into the stream
+    kernel (the lm_head plan from M = 5) or a top-k.  Workspace: the row
+    counters, then the per-workgroup keys (fused) or a logits buffer, then
+    the per-chunk lists."""
     al = lambda v: -(-v // 256) * 256
     N, K = 151936, 2560
-    for M, kernel in [(1, _lib.KERNEL_VALU), (4, _lib.KERNEL_VALU), (5, _lib.KERNEL_MFMA_LDS),
-                      (16, _lib.KERNEL_MFMA_LDS), (17, _lib.KERNEL_STREAM), (64, _lib.KERNEL_STREAM),
+    for M, kernel in [(1, _lib.KERNEL_VALU), (4, _lib.KERNEL_VALU), (5, _lib.KERNEL_STREAM),
+                      (16, _lib.KERNEL_STREAM), (17, _lib.KERNEL_STREAM), (64, _lib.KERNEL_STREAM),
                       (100, _lib.KERNEL_STREAM)]:
         Mc = min(M, 64)
         for k in (1, 8):
@@ -364,6 +365,12 @@ def test_select_plan_and_workspace(lib):
                 chunks = -(-N // 16384)
             want = 64 * 128 + src + al(Mc * chunks * k * 8)  # row counters 128 B apart
             assert lib.krk_gemm_select_workspace_bytes(M, N, K, k, None) == want, (M, k)
+    # An LDS-staged MFMA configuration with 256-k stages fuses argmax.
+    lds = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=2, unroll=3, k_chunk=256))
+    assert lib.krk_gemm_select_fused(8, N, K, 1, ctypes.byref(lds)) == 1
+    assert lib.krk_gemm_select_fused(8, N, K, 8, ctypes.byref(lds)) == 0
+    keys = al(8 * (-(-(N // 32) // 2) * 2) * 8) + al(8 * -(-(N // 32) // 1024) * 8)
+    assert lib.krk_gemm_select_workspace_bytes(8, N, K, 1, ctypes.byref(lds)) == 64 * 128 + keys
     # Any plain configuration is accepted: the stream kernel writes logits.
     stream = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_STREAM))
     assert lib.krk_gemm_select_workspace_bytes(8, N, K, 1, ctypes.byref(stream)) > 0

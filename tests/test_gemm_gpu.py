@@ -778,6 +778,21 @@ def test_select_lm_head(device, lm_head, lm_head_dev, M, k):
         "selection without logits differs"
 
 
+@pytest.mark.parametrize("M", [5, 16])
+def test_select_lm_head_fused_lds(device, lm_head, lm_head_dev, M):
+    """Argmax fused into an LDS-staged MFMA lm_head projection (a tuned
+    choice at these M; the table's plan there is the stream kernel)."""
+    cfg = dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=2, unroll=3, k_chunk=256, splits=1)
+    assert G.select_fused(M, R.VOCAB, R.HIDDEN, 1, cfg)
+    x = R.randn_bf16((M, R.HIDDEN), R.seed_for(5, M, "x") + 9)
+    say("select lm_head fused lds", M)
+    idx, vals, logits = krk_select(x, lm_head, 1, cfg, wd=lm_head_dev)
+    _check_selection(idx, vals, logits, 1, f"select fused lds M={M}")
+    ref = R.linear_bf16(x, lm_head)
+    assert_parity(logits, ref, f"select fused lds logits M={M}")
+    assert torch.equal(idx[:, 0], R.argmax_rows(ref)), f"select fused lds M={M}: argmax differs from the oracle's"
+
+
 def _tie_weights(N, K, seed):
     """W whose rows repeat: row 3·i + j = row 3·i for j < 3, so equal logits
     sit at consecutive indices; one row pair is NaN-producing."""
