@@ -131,7 +131,8 @@ int krk_gemm_plan(int M, int N, int K, int epilogue, krk_gemm_config* out);
 /*
  * krk_gemm_candidates — the search space of a warm-up tuner for this shape:
  * every distinct configuration the library accepts from a fixed grid (VALU
- * rows per wave x waves x splits for M <= 8, LDS-staged MFMA tiles x stages
+ * rows per wave x waves x splits x blocks in flight for M <= 8, LDS-staged
+ * MFMA tiles x stages
  * in flight x k per stage x splits, stream kernel depth x splits, register
  * MFMA tiles x splits), resolved as krk_gemm_bf16_config would resolve it,
  * krk_gemm_plan's configuration first.  Writes the first cap of them to out

@@ -94,8 +94,8 @@ struct TableEntry {
 constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits, int k_chunk = 0) {
     return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk};
 }
-// VALU entries: n_tiles = W rows per wave, unroll 0 = blocks in flight chosen
-// to cover a split's K range in one pass.  MFMA_LDS entries: unroll = stages in
+// VALU entries: n_tiles = W rows per wave, unroll = 512-k blocks in flight per
+// row (0: enough to cover a split's K range in one pass).  MFMA_LDS entries: unroll = stages in
 // flight, k_chunk 0 = 512 where it fits.
 const TableEntry kTable[] = {
     // qkv 2560 -> 6144
@@ -106,8 +106,7 @@ const TableEntry kTable[] = {
     // o_proj 4096 -> 2560
     {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 3, 8, kcfg(KRK_KERNEL_VALU, 2, 4, 8, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
     {2560, 4096, KRK_EPILOGUE_NONE, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
     {2560, 4096, KRK_EPILOGUE_NONE, 25, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
@@ -120,7 +119,9 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 2, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 2, 8, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     {2560, 9728, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 9728, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // lm_head 2560 -> 151936
@@ -216,7 +217,7 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
             if (c->kernel == KRK_KERNEL_VALU) {
                 c->m_tiles = valu_mx(Mc);
-                c->unroll = valu_depth(c->m_tiles, c->n_tiles, cdiv(KST, c->splits));
+                if (!c->unroll) c->unroll = valu_depth(c->m_tiles, c->n_tiles, cdiv(KST, c->splits));
             }
             return;
         }
@@ -1236,10 +1237,13 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
     add(plan);
     const int nts[] = {1, 2, 4};
     const int splits[] = {1, 2, 3, 4};
+    // VALU: unroll 0 covers a split's K range in one pass; 2 and 4 blocks in
+    // flight per row leave more waves resident (fewer VGPRs).
     if (Mc <= kValuMaxRows)
         for (int nt : nts)
             for (int wv : {4, krk::kValuMaxWaves})
-                for (int sp : splits) add(krk_gemm_config{KRK_KERNEL_VALU, 0, nt, 0, wv, sp, 0});
+                for (int sp : splits)
+                    for (int u : {0, 2, 4}) add(krk_gemm_config{KRK_KERNEL_VALU, 0, nt, u, wv, sp, 0});
     // More splits for the weight-streaming MFMA kernels: at M >= 16 they cut
     // each workgroup's share of x, the bound of narrow-N, long-K shapes.
     const int wide_splits[] = {1, 2, 3, 4, 6, 8};
