@@ -546,9 +546,9 @@ int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int XS, bool SILU>
-int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU>);
+template <int MT, int XS, bool SILU, bool SEL = false>
+int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {}) {
+    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SEL>);
     size_t shm = krk::stream_lds_bytes(MT, depth);
     const int G = stream_groups(nblocks, a.splits);
     // Unsplit K: the rest of the LDS holds finished blocks until the end.
@@ -568,7 +568,7 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     const int groups = G * a.splits;
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
                     (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth, (void*)&obcap,
-                    (void*)&a.part, (void*)&a.ctr};
+                    (void*)&a.part, (void*)&a.ctr, (void*)&sa};
     hipError_t e = hipLaunchKernel(fn, dim3(groups), dim3(64 * krk::kStreamWaves), args, shm, stream);
     return hip_status(e, "stream_gemm_kernel launch");
 }
@@ -596,6 +596,21 @@ int dispatch_stream_xs(const LaunchArgs& a, const krk_gemm_config& c, int nblock
         }
     }
     return fail(KRK_ERR_UNSUPPORTED, "STREAM has no x-register layout for m_tiles=%d and this K split", MT);
+}
+
+// The argmax epilogue of the stream kernel is instantiated for K in 5
+// stages (the hidden size 2560 the lm_head reads), K unsplit.
+constexpr int kStreamSelStages = 5;
+
+int dispatch_stream_sel(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                        const krk::SelectArgs& sa) {
+    switch (c.m_tiles) {
+        case 1: return launch_stream<1, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
+        case 2: return launch_stream<2, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
+        case 3: return launch_stream<3, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
+        case 4: return launch_stream<4, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
 
 template <bool SILU>
@@ -866,13 +881,12 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
 // ----------------------------------------------------------------- token selection
 // The lm_head projection followed by per-row argmax / top-k (krk_select.h).
 // Two plans:
-//   * fused (argmax behind a VALU or LDS-staged MFMA projection with unsplit
-//     K): the projection's epilogue writes one key per row and workgroup and
-//     select_rows_kernel reduces those keys; the logits are written only when
-//     the caller asks for them;
-//   * unfused (top-k, and every other projection plan, e.g. the stream kernel
-//     the table picks at M >= 17): the plain projection writes the bf16
-//     logits (to y, or to the workspace when y is null) and
+//   * fused (argmax behind a VALU, LDS-staged MFMA or stream projection with
+//     unsplit K): the projection's epilogue writes one key per row and
+//     workgroup and select_rows_kernel reduces those keys; the logits are
+//     written only when the caller asks for them;
+//   * unfused (top-k, and other projection plans): the plain projection
+//     writes the bf16 logits (to y, or to the workspace when y is null) and
 //     select_rows_kernel reduces them.
 // A top-k in the epilogue was measured and rejected: its per-workgroup
 // cross-lane rounds added 15-60% to the short projection workgroups, more
@@ -907,8 +921,9 @@ int dispatch_plain(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, h
 }
 
 // Whether argmax runs fused behind this projection plan (rows per launch Mc).
-bool select_fusable(const krk_gemm_config& c, int Mc) {
+bool select_fusable(const krk_gemm_config& c, int Mc, int K) {
     if (c.splits != 1) return false;
+    if (c.kernel == KRK_KERNEL_STREAM) return cdiv(K, krk::kStreamKC) == kStreamSelStages;
     if (c.kernel == KRK_KERNEL_VALU) return c.m_tiles <= kSelValuMaxRows && c.unroll == kValuNormDepth;
     if (c.kernel == KRK_KERNEL_MFMA_LDS)
         return c.k_chunk == 256 && (c.n_tiles == 2 || c.n_tiles == 4) && c.m_tiles >= cdiv(Mc, 16) &&
@@ -925,7 +940,7 @@ int select_plan_for(int M, int N, int K, int k, const krk_gemm_config* cfg, Sele
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     int rc = resolve_config(M, N, K, KRK_EPILOGUE_NONE, cfg, &out->c);
     if (rc) return rc;
-    out->fused = k == 1 && select_fusable(out->c, Mc);
+    out->fused = k == 1 && select_fusable(out->c, Mc, K);
     return KRK_OK;
 }
 
@@ -947,7 +962,10 @@ SelectLayout select_layout(int M, int N, int k, const SelectPlan& p) {
     size_t at = align_up(l.proj + workspace_for(Mc, N, KRK_EPILOGUE_NONE, p.c), 256);
     l.src = at;
     if (p.fused) {
-        l.n = geometry(Mc, N, KRK_EPILOGUE_NONE, p.c).nblocks;
+        // One key per row and projection workgroup (the stream kernel's
+        // workgroups each cover many blocks).
+        const int nb = geometry(Mc, N, KRK_EPILOGUE_NONE, p.c).nblocks;
+        l.n = p.c.kernel == KRK_KERNEL_STREAM ? stream_groups(nb, 1) : nb;
         l.ld = align_up((size_t)l.n, 2);
         at += align_up((size_t)Mc * l.ld * sizeof(uint64_t), 256);
         l.chunks = cdiv(l.n, krk::kSelChunkKeys);
@@ -1035,7 +1053,9 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
             a.y = y ? static_cast<uint16_t*>(y) + (int64_t)m0 * ldy : nullptr;
             a.ldy = ldy;
             const krk::SelectArgs sa{reinterpret_cast<uint64_t*>(ws + l.src), l.ld};
-            if (p.c.kernel == KRK_KERNEL_VALU) {
+            if (p.c.kernel == KRK_KERNEL_STREAM) {
+                rc = dispatch_stream_sel(a, p.c, g.nblocks, st, sa);
+            } else if (p.c.kernel == KRK_KERNEL_VALU) {
                 switch (p.c.m_tiles) {
                     case 1: rc = dispatch_valu_sel<1>(a, p.c, g.nblocks, st, sa); break;
                     case 2: rc = dispatch_valu_sel<2>(a, p.c, g.nblocks, st, sa); break;

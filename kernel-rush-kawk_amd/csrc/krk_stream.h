@@ -33,6 +33,7 @@
 #pragma once
 
 #include "krk_epilogue.h"
+#include "krk_select.h"
 #include "krk_sync.h"
 
 namespace krk {
@@ -57,14 +58,18 @@ __host__ __device__ constexpr size_t stream_out_bytes(int MT, bool silu) { retur
 
 // MT: 16-row m tiles (M <= 16·MT).  XS: most K stages a workgroup owns (its
 // x fragments live in X[XS][2][MT]).  SILU: gate/up blocks with the epilogue.
-template <int MT, int XS, bool SILU>
+// SEL (K unsplit): each workgroup keeps every row's largest (value, index)
+// key over its blocks (krk_select.h) and writes it to sa.keys[m][workgroup];
+// y (the logits) is written only when non-null.
+template <int MT, int XS, bool SILU, bool SEL = false>
 __global__ void __launch_bounds__(512)
 stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                    const uint16_t* __restrict__ w, int64_t ldw,
                    uint16_t* __restrict__ y, int64_t ldy,
                    int M, int N, int K, int splits, int depth, int obcap,
-                   float* __restrict__ part, uint32_t* __restrict__ ctr) {
+                   float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa) {
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
+    static_assert(!(SEL && SILU), "selection reads plain logits");
     constexpr int WV = kStreamWaves;
     constexpr int KPW = kStreamKPW;
     constexpr int LPW = kStreamLPW;
@@ -205,10 +210,16 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     // the partials) and its DMA issue, so the ring keeps streaming while it
     // works.  Partial layout: rb[wave][m tile][lane] f32x4, lane (r, q) holds
     // rows 4q..4q+3 of channel r.
+    // SEL: item slots a thread visits in finish_block (the same rows every
+    // block), each with its row's running largest key.
+    constexpr int kSelSlots = SEL ? (MT * 4 * (SILU ? 8 : 16) * 4 + 511) / 512 : 1;
+    uint64_t best[kSelSlots];
+#pragma unroll
+    for (int j = 0; j < kSelSlots; ++j) best[j] = 0;
     auto finish_block = [&](int bl, const f32x4* rb) {
         const int b = gi + bl * Gs;
         const int sl = obcap > 0 ? bl % obcap : 0;
-        if (splits == 1 && sl == 0 && bl > 0) {
+        if (splits == 1 && sl == 0 && bl > 0 && (!SEL || y)) {
             // Buffer full: write it out before slot 0 is reused.
             flush(bl - obcap, obcap);
             lds_wait();
@@ -239,7 +250,13 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             }
             const int c = b * CB + rr;
             if (splits == 1) {
-                ob[(size_t)(sl * MP + m) * CB + rr] = (uint16_t)(SILU ? silu_mul_bf16(g, u) : f32_to_bf16(g));
+                const uint32_t v = SILU ? silu_mul_bf16(g, u) : f32_to_bf16(g);
+                ob[(size_t)(sl * MP + m) * CB + rr] = (uint16_t)v;
+                if constexpr (SEL) {
+                    // Per lane: the largest key of its channel of row m over
+                    // the blocks so far (reduced across channels at the end).
+                    if (m < M && c < Nout) best[it / 512] = umax64(best[it / 512], sel_key(v, (uint32_t)c));
+                }
             } else if (m < M && c < Nout) {
                 o.put(m, c, g, u);
             }
@@ -288,11 +305,28 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     if (myblocks > 0) {
         bare_barrier();
         finish_block(myblocks - 1, ((myblocks - 1) & 1) ? red1 : red0);
-        if (splits == 1) {
+        if (splits == 1 && (!SEL || y)) {
             lds_wait();
             bare_barrier();
             const int base = (myblocks - 1) / obcap * obcap;
             flush(base, myblocks - base);
+        }
+    }
+    if constexpr (SEL) {
+        // Reduce each row's keys over its 16 channels (lane bits 2..5: the
+        // block size covers the items of one slot, so it and lane agree in
+        // bits 0..5); the lane with channel bits 0 writes the row's key.
+#pragma unroll
+        for (int j = 0; j < kSelSlots; ++j) {
+#pragma unroll
+            for (int off = 4; off < 64; off <<= 1) best[j] = umax64(best[j], shfl_xor_u64(best[j], off));
+            const int it = threadIdx.x + 512 * j;
+            const int e = it & 3;
+            const int qq = (it >> 6) & 3;  // item layout of finish_block (LS = 16)
+            const int i = it >> 8;
+            const int m = 16 * i + 4 * qq + e;
+            if (it < MT * 4 * 16 * 4 && ((it >> 2) & 15) == 0 && m < M)
+                store_agent_u64(sa.keys + (int64_t)m * sa.ldk + blockIdx.x, best[j]);
         }
     }
 }

@@ -336,12 +336,25 @@ def test_select_argument_errors(lib, kw, code, msg):
     assert msg in _lib.last_error()
 
 
+def _stream_groups(nblocks, cus=256):
+    """Workgroups of the persistent stream kernel for nblocks blocks, K unsplit."""
+    if nblocks <= cus:
+        return nblocks
+    best, best_eff = cus, 0.0
+    for g in range(cus, cus // 2 - 1, -1):
+        eff = nblocks / (-(-nblocks // g) * cus)
+        if eff > best_eff + 1e-9:
+            best, best_eff = g, eff
+    return best
+
+
 def test_select_plan_and_workspace(lib):
     """The projection plan is the plain table's; argmax fuses into the VALU
-    (M <= 4) plans and LDS-staged MFMA configurations, never into the stream
-    kernel (the lm_head plan from M = 5) or a top-k.  Workspace: the row
-    counters, then the per-workgroup keys (fused) or a logits buffer, then
-    the per-chunk lists."""
+    (M <= 4) and stream (from M = 5, K of 5 stages) plans and into
+    LDS-staged MFMA configurations, never into a top-k.  Workspace: the row
+    counters, then one key per row and projection workgroup (fused; the
+    stream kernel's workgroups each cover many blocks) or a logits buffer,
+    then the per-chunk lists."""
     al = lambda v: -(-v // 256) * 256
     N, K = 151936, 2560
     for M, kernel in [(1, _lib.KERNEL_VALU), (4, _lib.KERNEL_VALU), (5, _lib.KERNEL_STREAM),
@@ -355,9 +368,11 @@ def test_select_plan_and_workspace(lib):
             c = cfg.as_dict()
             assert c == plain.as_dict() and c["kernel"] == kernel, (M, k, c)
             fused = lib.krk_gemm_select_fused(M, N, K, k, None)
-            assert fused == int(k == 1 and kernel != _lib.KERNEL_STREAM), (M, k)
+            assert fused == int(k == 1), (M, k)
             if fused:
                 G = -(-N // _channels_per_block(c, NONE))
+                if kernel == _lib.KERNEL_STREAM:
+                    G = _stream_groups(G)
                 src = al(Mc * (-(-G // 2) * 2) * 8)  # one key per row and workgroup
                 chunks = -(-G // 1024)
             else:
@@ -371,10 +386,14 @@ def test_select_plan_and_workspace(lib):
     assert lib.krk_gemm_select_fused(8, N, K, 8, ctypes.byref(lds)) == 0
     keys = al(8 * (-(-(N // 32) // 2) * 2) * 8) + al(8 * -(-(N // 32) // 1024) * 8)
     assert lib.krk_gemm_select_workspace_bytes(8, N, K, 1, ctypes.byref(lds)) == 64 * 128 + keys
-    # Any plain configuration is accepted: the stream kernel writes logits.
+    # Any plain configuration is accepted; the stream kernel fuses argmax only
+    # for a K of 5 stages and unsplit.
     stream = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_STREAM))
     assert lib.krk_gemm_select_workspace_bytes(8, N, K, 1, ctypes.byref(stream)) > 0
-    assert lib.krk_gemm_select_fused(8, N, K, 1, ctypes.byref(stream)) == 0
+    assert lib.krk_gemm_select_fused(8, N, K, 1, ctypes.byref(stream)) == 1
+    assert lib.krk_gemm_select_fused(8, N, 1536, 1, ctypes.byref(stream)) == 0
+    stream2 = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_STREAM, splits=2))
+    assert lib.krk_gemm_select_fused(8, N, K, 1, ctypes.byref(stream2)) == 0
     # A split-K projection reserves its partials after the counters.
     split = GemmConfig.from_dict(dict(kernel=_lib.KERNEL_VALU, splits=2))
     c = GemmConfig()
