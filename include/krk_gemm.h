@@ -232,7 +232,8 @@ int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd
  * idx[m][0..k) = indices of the k largest bf16 logits bf16(x[m]·W[n]ᵀ) of
  * row m, largest first, equal values at the lower index first (NaN above
  * +inf, -0 equal to +0).  For k = 1 behind a VALU, LDS-staged MFMA or
- * stream projection (krk_gemm_select_fused) the projection's epilogue reduces its
+ * stream projection, and for k > 1 behind a stream projection of up to 16
+ * rows (krk_gemm_select_fused), the projection's epilogue reduces its
  * outputs to one key per row and workgroup and the logits are not written
  * unless y is given; otherwise the plain projection writes the logits (to y,
  * or to the workspace) and a selection kernel reads them back.  Either way

@@ -546,9 +546,9 @@ int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int XS, bool SILU, bool SEL = false>
+template <int MT, int XS, bool SILU, int SK = 0>
 int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {}) {
-    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SEL>);
+    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK>);
     size_t shm = krk::stream_lds_bytes(MT, depth);
     const int G = stream_groups(nblocks, a.splits);
     // Unsplit K: the rest of the LDS holds finished blocks until the end.
@@ -598,19 +598,26 @@ int dispatch_stream_xs(const LaunchArgs& a, const krk_gemm_config& c, int nblock
     return fail(KRK_ERR_UNSUPPORTED, "STREAM has no x-register layout for m_tiles=%d and this K split", MT);
 }
 
-// The argmax epilogue of the stream kernel is instantiated for K in 5
-// stages (the hidden size 2560 the lm_head reads), K unsplit.
+// The selection epilogue of the stream kernel is instantiated for K in 5
+// stages (the hidden size 2560 the lm_head reads), K unsplit: argmax at every
+// M, top-kSelMaxK up to 16 rows.  Measured (lm_head): the running top-8 lists
+// add 3.5 us to the projection at M <= 16, against 6.4 us saved by reading
+// keys instead of logits; at 32 rows they add 11.6 us, more than they save.
 constexpr int kStreamSelStages = 5;
+constexpr int kStreamTopkMaxTiles = 1;
 
+template <int SK>
 int dispatch_stream_sel(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
                         const krk::SelectArgs& sa) {
-    switch (c.m_tiles) {
-        case 1: return launch_stream<1, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
-        case 2: return launch_stream<2, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
-        case 3: return launch_stream<3, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
-        case 4: return launch_stream<4, kStreamSelStages, false, true>(a, nblocks, c.unroll, s, sa);
+    if (c.m_tiles == 1) return launch_stream<1, kStreamSelStages, false, SK>(a, nblocks, c.unroll, s, sa);
+    if constexpr (SK == 1) {
+        switch (c.m_tiles) {
+            case 2: return launch_stream<2, kStreamSelStages, false, 1>(a, nblocks, c.unroll, s, sa);
+            case 3: return launch_stream<3, kStreamSelStages, false, 1>(a, nblocks, c.unroll, s, sa);
+            case 4: return launch_stream<4, kStreamSelStages, false, 1>(a, nblocks, c.unroll, s, sa);
+        }
     }
-    return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
+    return fail(KRK_ERR_UNSUPPORTED, "STREAM selection epilogue: m_tiles=%d", c.m_tiles);
 }
 
 template <bool SILU>
@@ -881,8 +888,9 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
 // ----------------------------------------------------------------- token selection
 // The lm_head projection followed by per-row argmax / top-k (krk_select.h).
 // Two plans:
-//   * fused (argmax behind a VALU, LDS-staged MFMA or stream projection with
-//     unsplit K): the projection's epilogue writes one key per row and
+//   * fused (argmax behind a VALU, LDS-staged MFMA or stream projection, and
+//     top-k behind a stream projection of up to 16 rows, K unsplit): the
+//     projection's epilogue writes one key (top-k: kSelMaxK keys) per row and
 //     workgroup and select_rows_kernel reduces those keys; the logits are
 //     written only when the caller asks for them;
 //   * unfused (top-k, and other projection plans): the plain projection
@@ -921,9 +929,11 @@ int dispatch_plain(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, h
 }
 
 // Whether argmax runs fused behind this projection plan (rows per launch Mc).
-bool select_fusable(const krk_gemm_config& c, int Mc, int K) {
+bool select_fusable(const krk_gemm_config& c, int Mc, int K, int k) {
     if (c.splits != 1) return false;
-    if (c.kernel == KRK_KERNEL_STREAM) return cdiv(K, krk::kStreamKC) == kStreamSelStages;
+    if (c.kernel == KRK_KERNEL_STREAM)
+        return cdiv(K, krk::kStreamKC) == kStreamSelStages && (k == 1 || c.m_tiles <= kStreamTopkMaxTiles);
+    if (k != 1) return false;
     if (c.kernel == KRK_KERNEL_VALU) return c.m_tiles <= kSelValuMaxRows && c.unroll == kValuNormDepth;
     if (c.kernel == KRK_KERNEL_MFMA_LDS)
         return c.k_chunk == 256 && (c.n_tiles == 2 || c.n_tiles == 4) && c.m_tiles >= cdiv(Mc, 16) &&
@@ -940,7 +950,7 @@ int select_plan_for(int M, int N, int K, int k, const krk_gemm_config* cfg, Sele
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     int rc = resolve_config(M, N, K, KRK_EPILOGUE_NONE, cfg, &out->c);
     if (rc) return rc;
-    out->fused = k == 1 && select_fusable(out->c, Mc, K);
+    out->fused = select_fusable(out->c, Mc, K, k);
     return KRK_OK;
 }
 
@@ -965,7 +975,7 @@ SelectLayout select_layout(int M, int N, int k, const SelectPlan& p) {
         // One key per row and projection workgroup (the stream kernel's
         // workgroups each cover many blocks).
         const int nb = geometry(Mc, N, KRK_EPILOGUE_NONE, p.c).nblocks;
-        l.n = p.c.kernel == KRK_KERNEL_STREAM ? stream_groups(nb, 1) : nb;
+        l.n = p.c.kernel == KRK_KERNEL_STREAM ? stream_groups(nb, 1) * (k == 1 ? 1 : krk::kSelMaxK) : nb;
         l.ld = align_up((size_t)l.n, 2);
         at += align_up((size_t)Mc * l.ld * sizeof(uint64_t), 256);
         l.chunks = cdiv(l.n, krk::kSelChunkKeys);
@@ -1054,7 +1064,8 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
             a.ldy = ldy;
             const krk::SelectArgs sa{reinterpret_cast<uint64_t*>(ws + l.src), l.ld};
             if (p.c.kernel == KRK_KERNEL_STREAM) {
-                rc = dispatch_stream_sel(a, p.c, g.nblocks, st, sa);
+                rc = k == 1 ? dispatch_stream_sel<1>(a, p.c, g.nblocks, st, sa)
+                            : dispatch_stream_sel<krk::kSelMaxK>(a, p.c, g.nblocks, st, sa);
             } else if (p.c.kernel == KRK_KERNEL_VALU) {
                 switch (p.c.m_tiles) {
                     case 1: rc = dispatch_valu_sel<1>(a, p.c, g.nblocks, st, sa); break;
@@ -1075,7 +1086,8 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
             ra.src = sa.keys;
             ra.ld = l.ld;
             ra.vec = 1;
-            rc = launch_select_rows<1, true>(ra, l.chunks, a.M, st);
+            rc = k == 1 ? launch_select_rows<1, true>(ra, l.chunks, a.M, st)
+                        : launch_select_rows<krk::kSelMaxK, true>(ra, l.chunks, a.M, st);
         } else {
             uint16_t* logits = y ? static_cast<uint16_t*>(y) + (int64_t)m0 * ldy : reinterpret_cast<uint16_t*>(ws + l.src);
             a.y = logits;

@@ -240,7 +240,8 @@ __device__ __forceinline__ void rank_select(const uint64_t* cand, int cnt, int k
 }
 
 // Grid (chunks, M): KM = 1 (argmax) or kSelMaxK (top-k, k <= KM); KEYS: src
-// holds keys (argmax only) instead of bf16 logits.
+// holds keys (one per row and projection workgroup for argmax, kSelMaxK per
+// workgroup for top-k) instead of bf16 logits.
 //
 // Logits: a chunk of kSelChunkVals values, kSelVec 16-byte vectors per thread
 // held in registers.  Pass 1 takes the ord2 maximum of every group of
@@ -254,7 +255,6 @@ __device__ __forceinline__ void rank_select(const uint64_t* cand, int cnt, int k
 // thread inserts its keys into a sorted list and the lists meet in block_top.
 template <int KM, bool KEYS>
 __global__ void __launch_bounds__(kSelThreads) select_rows_kernel(RowSelectArgs a) {
-    static_assert(!KEYS || KM == 1, "key sources carry one key per row and workgroup");
     __shared__ uint64_t lds[kSelThreads / 64 * KM];
     __shared__ uint64_t cand[kSelCap];
     __shared__ uint64_t res[kSelMaxK];
@@ -289,7 +289,14 @@ __global__ void __launch_bounds__(kSelThreads) select_rows_kernel(RowSelectArgs 
             }
         }
 #pragma unroll
-        for (int u = 0; u < kSelKeyVec; ++u) top[0] = umax64(top[0], umax64(v[u][0], v[u][1]));
+        for (int u = 0; u < kSelKeyVec; ++u) {
+            if constexpr (KM == 1) {
+                top[0] = umax64(top[0], umax64(v[u][0], v[u][1]));
+            } else {
+                topk_insert(top, v[u][0]);
+                topk_insert(top, v[u][1]);
+            }
+        }
         block_top(top, lds);
     } else {
         const uint16_t* row = static_cast<const uint16_t*>(a.src) + (int64_t)m * a.ld;

@@ -58,10 +58,11 @@ __host__ __device__ constexpr size_t stream_out_bytes(int MT, bool silu) { retur
 
 // MT: 16-row m tiles (M <= 16·MT).  XS: most K stages a workgroup owns (its
 // x fragments live in X[XS][2][MT]).  SILU: gate/up blocks with the epilogue.
-// SEL (K unsplit): each workgroup keeps every row's largest (value, index)
-// key over its blocks (krk_select.h) and writes it to sa.keys[m][workgroup];
-// y (the logits) is written only when non-null.
-template <int MT, int XS, bool SILU, bool SEL = false>
+// SK (K unsplit): 1 or kSelMaxK — each workgroup keeps every row's SK
+// largest (value, index) keys over its blocks (krk_select.h) and writes them
+// to sa.keys[m][workgroup * SK ...]; y (the logits) is written only when
+// non-null.  0: no selection.
+template <int MT, int XS, bool SILU, int SK = 0>
 __global__ void __launch_bounds__(512)
 stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                    const uint16_t* __restrict__ w, int64_t ldw,
@@ -69,7 +70,9 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                    int M, int N, int K, int splits, int depth, int obcap,
                    float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa) {
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
+    constexpr bool SEL = SK > 0;
     static_assert(!(SEL && SILU), "selection reads plain logits");
+    static_assert(SK == 0 || SK == 1 || SK == kSelMaxK, "argmax or top-kSelMaxK");
     constexpr int WV = kStreamWaves;
     constexpr int KPW = kStreamKPW;
     constexpr int LPW = kStreamLPW;
@@ -213,9 +216,12 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     // SEL: item slots a thread visits in finish_block (the same rows every
     // block), each with its row's running largest key.
     constexpr int kSelSlots = SEL ? (MT * 4 * (SILU ? 8 : 16) * 4 + 511) / 512 : 1;
-    uint64_t best[kSelSlots];
+    constexpr int KL = SK > 0 ? SK : 1;  // keys kept per slot, descending
+    uint64_t best[kSelSlots][KL];
 #pragma unroll
-    for (int j = 0; j < kSelSlots; ++j) best[j] = 0;
+    for (int j = 0; j < kSelSlots; ++j)
+#pragma unroll
+        for (int q2 = 0; q2 < KL; ++q2) best[j][q2] = 0;
     auto finish_block = [&](int bl, const f32x4* rb) {
         const int b = gi + bl * Gs;
         const int sl = obcap > 0 ? bl % obcap : 0;
@@ -255,7 +261,11 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 if constexpr (SEL) {
                     // Per lane: the largest key of its channel of row m over
                     // the blocks so far (reduced across channels at the end).
-                    if (m < M && c < Nout) best[it / 512] = umax64(best[it / 512], sel_key(v, (uint32_t)c));
+                    if (m < M && c < Nout) {
+                        const uint64_t key = sel_key(v, (uint32_t)c);
+                        if constexpr (SK == 1) best[it / 512][0] = umax64(best[it / 512][0], key);
+                        else topk_insert(best[it / 512], key);
+                    }
                 }
             } else if (m < M && c < Nout) {
                 o.put(m, c, g, u);
@@ -319,14 +329,20 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
         for (int j = 0; j < kSelSlots; ++j) {
 #pragma unroll
-            for (int off = 4; off < 64; off <<= 1) best[j] = umax64(best[j], shfl_xor_u64(best[j], off));
+            for (int off = 4; off < 64; off <<= 1) {
+                if constexpr (SK == 1) best[j][0] = umax64(best[j][0], shfl_xor_u64(best[j][0], off));
+                else xor_level(best[j], off);
+            }
             const int it = threadIdx.x + 512 * j;
             const int e = it & 3;
             const int qq = (it >> 6) & 3;  // item layout of finish_block (LS = 16)
             const int i = it >> 8;
             const int m = 16 * i + 4 * qq + e;
-            if (it < MT * 4 * 16 * 4 && ((it >> 2) & 15) == 0 && m < M)
-                store_agent_u64(sa.keys + (int64_t)m * sa.ldk + blockIdx.x, best[j]);
+            if (it < MT * 4 * 16 * 4 && ((it >> 2) & 15) == 0 && m < M) {
+#pragma unroll
+                for (int q2 = 0; q2 < KL; ++q2)
+                    store_agent_u64(sa.keys + (int64_t)m * sa.ldk + (int64_t)blockIdx.x * KL + q2, best[j][q2]);
+            }
         }
     }
 }

@@ -465,7 +465,8 @@ def select_plan(M: int, N: int, K: int, k: int = 1) -> dict:
 
 def select_fused(M: int, N: int, K: int, k: int = 1, config: dict | None = None) -> bool:
     """Whether the selection runs in the projection's epilogue (argmax behind
-    a VALU, LDS-staged MFMA or stream projection: the logits are then not written
+    a VALU, LDS-staged MFMA or stream projection, top-k behind a stream
+    projection of up to 16 rows: the logits are then not written
     unless asked for) rather than in a kernel that reads the logits back."""
     cfg = GemmConfig.from_dict(config) if config else None
     rc = _lib.load().krk_gemm_select_fused(M, N, K, k, ctypes.byref(cfg) if cfg else None)
@@ -479,9 +480,10 @@ class SkinnySelect:
     ``a @ w.T`` (largest first, equal values at the lower index first, NaN
     above everything).  ``k = 1`` is ``(a @ w.T).argmax(dim=-1, keepdim=True)``
     (engine/engine.py:196), ``k = 8`` the ``torch.topk(logits, 8).indices`` of
-    engine/recycle.py:170.  Argmax behind the VALU, LDS-staged MFMA and stream plans
-    runs in the projection's epilogue (``fused``) and writes no logits unless
-    ``logits`` is given; other plans write the logits and select from them.
+    engine/recycle.py:170.  Argmax behind the VALU, LDS-staged MFMA and stream
+    plans, and top-k behind stream plans of up to 16 rows, run in the
+    projection's epilogue (``fused``) and write no logits unless ``logits``
+    is given; other plans write the logits and select from them.
     ``config`` is the projection's configuration (any plain-epilogue one).
     The workspace belongs to the object (zero-filled once; calls leave it so)."""
 

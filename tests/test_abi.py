@@ -351,8 +351,9 @@ def _stream_groups(nblocks, cus=256):
 def test_select_plan_and_workspace(lib):
     """The projection plan is the plain table's; argmax fuses into the VALU
     (M <= 4) and stream (from M = 5, K of 5 stages) plans and into
-    LDS-staged MFMA configurations, never into a top-k.  Workspace: the row
-    counters, then one key per row and projection workgroup (fused; the
+    LDS-staged MFMA configurations; top-k fuses into stream plans of up to
+    16 rows only.  Workspace: the row counters, then the keys of each row
+    and projection workgroup (fused: one for argmax, 8 for top-k; the
     stream kernel's workgroups each cover many blocks) or a logits buffer,
     then the per-chunk lists."""
     al = lambda v: -(-v // 256) * 256
@@ -368,11 +369,11 @@ def test_select_plan_and_workspace(lib):
             c = cfg.as_dict()
             assert c == plain.as_dict() and c["kernel"] == kernel, (M, k, c)
             fused = lib.krk_gemm_select_fused(M, N, K, k, None)
-            assert fused == int(k == 1), (M, k)
+            assert fused == int(k == 1 or (kernel == _lib.KERNEL_STREAM and Mc <= 16)), (M, k)
             if fused:
                 G = -(-N // _channels_per_block(c, NONE))
                 if kernel == _lib.KERNEL_STREAM:
-                    G = _stream_groups(G)
+                    G = _stream_groups(G) * (1 if k == 1 else 8)
                 src = al(Mc * (-(-G // 2) * 2) * 8)  # one key per row and workgroup
                 chunks = -(-G // 1024)
             else:
