@@ -206,15 +206,8 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             }
         }
     };
-    // Block epilogue: each thread finishes output elements (m, c) of the
-    // block, summing the eight waves' partials in fixed wave order (8 or 16
-    // independent LDS reads, then the adds).  It runs inside the next
-    // block's first stage, after that stage's barrier (which also publishes
-    // the partials) and its DMA issue, so the ring keeps streaming while it
-    // works.  Partial layout: rb[wave][m tile][lane] f32x4, lane (r, q) holds
-    // rows 4q..4q+3 of channel r.
     // SEL: item slots a thread visits in finish_block (the same rows every
-    // block), each with its row's running largest key.
+    // block), each with its (row, channel)'s running largest keys.
     constexpr int kSelSlots = SEL ? (MT * 4 * (SILU ? 8 : 16) * 4 + 511) / 512 : 1;
     constexpr int KL = SK > 0 ? SK : 1;  // keys kept per slot, descending
     uint64_t best[kSelSlots][KL];
@@ -222,6 +215,13 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     for (int j = 0; j < kSelSlots; ++j)
 #pragma unroll
         for (int q2 = 0; q2 < KL; ++q2) best[j][q2] = 0;
+    // Block epilogue: each thread finishes output elements (m, c) of the
+    // block, summing the eight waves' partials in fixed wave order (8 or 16
+    // independent LDS reads, then the adds).  It runs inside the next
+    // block's first stage, after that stage's barrier (which also publishes
+    // the partials) and its DMA issue, so the ring keeps streaming while it
+    // works.  Partial layout: rb[wave][m tile][lane] f32x4, lane (r, q) holds
+    // rows 4q..4q+3 of channel r.
     auto finish_block = [&](int bl, const f32x4* rb) {
         const int b = gi + bl * Gs;
         const int sl = obcap > 0 ? bl % obcap : 0;
@@ -325,7 +325,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     if constexpr (SEL) {
         // Reduce each row's keys over its 16 channels (lane bits 2..5: the
         // block size covers the items of one slot, so it and lane agree in
-        // bits 0..5); the lane with channel bits 0 writes the row's key.
+        // bits 0..5); the lane of channel 0 writes the row's keys.
 #pragma unroll
         for (int j = 0; j < kSelSlots; ++j) {
 #pragma unroll
