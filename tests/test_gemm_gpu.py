@@ -822,7 +822,7 @@ def test_select_ties_nan_and_configs(device, M, N, K):
              dict(kernel=_lib.KERNEL_MFMA, splits=1)]
     base = {}
     for cfg in cfgs:
-        for k in (1, 8):
+        for k in (1, 3, 8):
             say("select ties", M, N, K, k, cfg)
             try:
                 idx, vals, logits = krk_select(x, w, k, cfg)
