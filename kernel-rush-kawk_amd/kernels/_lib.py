@@ -119,6 +119,22 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_tag = None
+
+
+def library_tag() -> str:
+    """A short digest of the loaded library file: tuned configurations are
+    cached under it, so a rebuilt library never reuses another build's
+    choices (a configuration may be slower, or no longer instantiated)."""
+    global _tag
+    with _lock:
+        if _tag is None:
+            import hashlib
+
+            _tag = hashlib.sha1(LIB_PATH.read_bytes()).hexdigest()[:12]
+    return _tag
+
+
 def last_error() -> str:
     return load().krk_last_error().decode(errors="replace")
 

@@ -16,9 +16,10 @@ as a graph replay over every layer's copy of the weight
   (gemm.py:548); a rejected candidate is logged and skipped (it would be a
   kernel bug: every configuration computes the same function);
 * timing is ``gemm._time`` (graph replay, median of 5, rotating weights);
-* results go to a ``TuneCache`` keyed by GPU architecture, kind and shape,
-  optionally persisted as JSON (``KRK_TUNE_CACHE``), so a serving process
-  tunes once per shape and later processes start from the file.
+* results go to a ``TuneCache`` keyed by GPU architecture, library build,
+  kind and shape, optionally persisted as JSON (``KRK_TUNE_CACHE``), so a
+  serving process tunes once per shape and later processes with the same
+  library start from the file.
 
 The winner is always a HIP configuration: torch is not a candidate, so a
 tuned call never leaves the native path.
@@ -68,8 +69,9 @@ class TuneCache:
 
     @staticmethod
     def key(device, kind: str, M: int, N: int, K: int) -> str:
+        """GPU architecture, library build (``_lib.library_tag``), kind and shape."""
         arch = torch.cuda.get_device_properties(torch.device(device)).gcnArchName.split(":")[0]
-        return f"{arch}/{kind}/M{M}/N{N}/K{K}"
+        return f"{arch}/{_lib.library_tag()}/{kind}/M{M}/N{N}/K{K}"
 
     def get(self, key: str) -> dict | None:
         with self._lock:

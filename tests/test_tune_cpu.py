@@ -39,3 +39,17 @@ def test_cache_memory_and_file(tmp_path):
     again = TuneCache(str(path))
     assert again.get("gfx950/gateup/M32/N19456/K2560") == cfg
     assert set(again.entries()) == set(data)
+
+
+def test_cache_key_names_the_library_build(monkeypatch):
+    """Entries are keyed by architecture, library digest, kind and shape, so a
+    rebuilt library never reuses another build's tuned configurations."""
+    from kernels import _lib, tune
+
+    class Props:
+        gcnArchName = "gfx950:sramecc+:xnack-"
+
+    monkeypatch.setattr(tune.torch.cuda, "get_device_properties", lambda dev: Props())
+    tag = _lib.library_tag()
+    assert len(tag) == 12 and tag == _lib.library_tag()
+    assert TuneCache.key("cuda:0", "matmul", 1, 6144, 2560) == f"gfx950/{tag}/matmul/M1/N6144/K2560"
