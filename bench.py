@@ -65,34 +65,6 @@ def randn_bf16(torch, shape, seed, scale, device):
     return t.mul_(scale).to(torch.bfloat16)
 
 
-def graph_time_ms(torch, calls, reps: int = 5):
-    """Median over ``reps`` replays of one graph holding ``calls`` (a list of
-    closures), divided by len(calls): milliseconds per call."""
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for c in calls[:3]:
-            c()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for c in calls:
-            c()
-    g.replay()
-    torch.cuda.synchronize()
-    samples = []
-    for _ in range(reps):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        samples.append(a.elapsed_time(b) / len(calls))
-    samples.sort()
-    return samples[len(samples) // 2], g
-
-
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +92,7 @@ def main() -> int:
     import torch.nn.functional as F
 
     from kernels import gemm as G
+    from kernels.timing import GraphReplay, replay_ms
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -207,7 +180,7 @@ def main() -> int:
     # back-to-back launches over the 36 distinct layer weights.
     dom = "gate_up"
     dom_calls = [(lambda L=L: ops[dom].run(x[dom], L[dom], outs[dom])) for L in layers]
-    dom_ms, _ = graph_time_ms(torch, dom_calls, reps=max(5, args.steps // 4))
+    dom_ms = replay_ms(dom_calls, reps=max(5, args.steps // 4))
     dom_bytes = algo_bytes(dom, M)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic = measured_traffic(dom, M, ops[dom].resolved_config)
@@ -230,7 +203,7 @@ def main() -> int:
                 ws = lm if name == "lm_head" else [L[name] for L in layers]
                 n = 2 * len(ws) if name == "lm_head" else len(ws)
                 calls = [(lambda w=ws[i % len(ws)]: op.run(xt, w, ot)) for i in range(n)]
-                ms, _ = graph_time_ms(torch, calls)
+                ms = replay_ms(calls)
                 row = {"shape": name, "M": Mt, "us": round(ms * 1000, 2),
                        "GBps": round(algo_bytes(name, Mt) / (ms * 1e-3) / 1e9, 1)}
                 row["pct_peak"] = round(100 * row["GBps"] / HBM_PEAK_GBPS, 1)
@@ -241,7 +214,7 @@ def main() -> int:
                                   for i in range(n)]
                     else:
                         tcalls = [(lambda w=ws[i % len(ws)]: F.linear(xt, w)) for i in range(n)]
-                    tms, _ = graph_time_ms(torch, tcalls)
+                    tms = replay_ms(tcalls)
                     row["torch_gpu_us"] = round(tms * 1000, 2)
                 table.append(row)
                 log(f"M={Mt:3d} {name:8s} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s {row['pct_peak']:5.1f}%"
@@ -269,7 +242,7 @@ def main() -> int:
                 op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
                 ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
                 calls = [(lambda w=w: op.run(xt, w, ot)) for w in wsh]
-                ms, _ = graph_time_ms(torch, calls)
+                ms = replay_ms(calls)
                 B.start(3.0)
                 try:
                     tuned = G.tune_projection(xt, wsh[0], epi, ws=wsh, cache=T.TuneCache())
@@ -285,7 +258,7 @@ def main() -> int:
                         tc = [(lambda w=w: (lambda r: F.silu(r[:, :Nw // 2]) * r[:, Nw // 2:])(F.linear(xt, w))) for w in wsh]
                     else:
                         tc = [(lambda w=w: F.linear(xt, w)) for w in wsh]
-                    tms, _ = graph_time_ms(torch, tc)
+                    tms = replay_ms(tc)
                     row["torch_gpu_us"] = round(tms * 1000, 2)
                 shards.append(row)
                 log(f"tp8 shard {name:8s} M={Mt:3d} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s   tuned {row['tuned_us']:8.2f} us"
@@ -313,9 +286,9 @@ def main() -> int:
                 ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
                 ws = lm if name == "lm_head" else [L[name] for L in layers]
                 n = 2 * len(ws) if name == "lm_head" else len(ws)
-                fused_ms, _ = graph_time_ms(torch, [(lambda w=ws[i % len(ws)]: op.run(xt, w, ot, norm=(yt, wn, xo, eps)))
+                fused_ms = replay_ms([(lambda w=ws[i % len(ws)]: op.run(xt, w, ot, norm=(yt, wn, xo, eps)))
                                                     for i in range(n)])
-                two_ms, _ = graph_time_ms(torch, [(lambda w=ws[i % len(ws)]: op.run(G.add_rms_norm(xt, yt, wn, eps, xout=xo), w, ot))
+                two_ms = replay_ms([(lambda w=ws[i % len(ws)]: op.run(G.add_rms_norm(xt, yt, wn, eps, xout=xo), w, ot))
                                                   for i in range(n)])
                 row = {"shape": name, "M": Mt, "us": round(fused_ms * 1000, 2),
                        "prologue_kernel_plus_gemm_us": round(two_ms * 1000, 2),
@@ -328,7 +301,7 @@ def main() -> int:
                                * wn.float()).to(torch.bfloat16)
                         r = F.linear(nrm, w)
                         return F.silu(r[:, :INTER]) * r[:, INTER:] if silu else r
-                    tms, _ = graph_time_ms(torch, [(lambda w=ws[i % len(ws)]: torch_normed(w)) for i in range(n)])
+                    tms = replay_ms([(lambda w=ws[i % len(ws)]: torch_normed(w)) for i in range(n)])
                     row["torch_gpu_us"] = round(tms * 1000, 2)
                 normed.append(row)
                 log(f"normed M={Mt:3d} {name:8s} {row['us']:8.2f} us ({'1 launch' if row['one_launch'] else '2 launches'})"
@@ -352,12 +325,12 @@ def main() -> int:
                 op = G.SkinnySelect(Mt, Nw, K, dev, k)
                 idx = torch.empty((Mt, k), dtype=torch.int64, device=dev)
                 n = 2 * len(lm)
-                f_ms, _ = graph_time_ms(torch, [(lambda w=lm[i % len(lm)]: op.run(xt, w, idx)) for i in range(n)])
+                f_ms = replay_ms([(lambda w=lm[i % len(lm)]: op.run(xt, w, idx)) for i in range(n)])
                 if k == 1:
                     sel = lambda: torch.argmax(lg, dim=-1)
                 else:
                     sel = lambda: torch.topk(lg, k, dim=-1).indices
-                u_ms, _ = graph_time_ms(torch, [(lambda w=lm[i % len(lm)]: (plain.run(xt, w, lg), sel())) for i in range(n)])
+                u_ms = replay_ms([(lambda w=lm[i % len(lm)]: (plain.run(xt, w, lg), sel())) for i in range(n)])
                 row = {"M": Mt, "k": k, "us": round(f_ms * 1000, 2), "plain_gemm_plus_torch_select_us": round(u_ms * 1000, 2),
                        "fused": op.fused, "config": op.resolved_config}
                 select.append(row)
@@ -415,7 +388,7 @@ def main() -> int:
                 "d": [(lambda Lm=Lm: mm["d"](act, Lm.wd)) for Lm in model.layers],
                 "lm": [(lambda w=w: mm["lm"](xs, yy, model.final_norm, xo, w)) for w in lm * 4],
             }
-            iso = {k: graph_time_ms(torch, v)[0] * 1000 for k, v in per.items()}
+            iso = {k: replay_ms(v) * 1000 for k, v in per.items()}
             iso_sum = LAYERS * (iso["qkv"] + iso["o"] + iso["gu"] + iso["d"]) + iso["lm"]
             row = {"M": Mt, "calls": st.calls, "us_per_step": round(step_us, 1),
                    "isolated_sum_us": round(iso_sum, 1),
@@ -440,7 +413,7 @@ def main() -> int:
                         cur = xb_
                     return F.linear(rms(cur, yv, model.final_norm, xa_), model.lm_head)
 
-                tms, _ = graph_time_ms(torch, [torch_step], reps=5)
+                tms = replay_ms([torch_step], reps=5)
                 row["torch_us_per_step"] = round(tms * 1000, 1)
             step_rows.append(row)
             log(f"decode step M={Mt:3d}: {row['us_per_step']:8.1f} us/step ({st.calls} calls), isolated sum "
@@ -507,7 +480,7 @@ def profile_shape(torch, G, dev, name: str, M: int) -> int:
     projection over distinct weights (the 36 layer weights of the sweep; for
     lm_head 2 copies, 8 launches), then 4 copies of a 256 MiB buffer for the
     counters' byte calibration.  Prints the configuration and the event-timed
-    µs per launch of the graph (median of 3 replays after 10 warm-up ones)."""
+    µs per launch of the graph (median of 3 replays after 9 untimed ones)."""
     K, Nw, silu = SHAPES[name]
     if name == "lm_head":
         ws = [randn_bf16(torch, (Nw, K), seed_for(4, 99, "lm_head") + i, 0.02, dev) for i in range(2)] * 4
@@ -517,10 +490,12 @@ def profile_shape(torch, G, dev, name: str, M: int) -> int:
     op = G.SkinnyGateUp(M, Nw // 2, K, dev) if silu else G.SkinnyMatmul(M, Nw, K, dev)
     out = torch.empty((M, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
     calls = [(lambda w=w: op.run(x, w, out)) for w in ws]
-    _, g = graph_time_ms(torch, calls, reps=1)
+    from kernels.timing import GraphReplay
+
+    replay = GraphReplay(calls)  # 3 eager warm-up calls, then the capture and one replay
     for _ in range(8):  # bring the clocks up before the timed replays
-        g.replay()
-    ms, _ = graph_time_ms(torch, calls, reps=3)
+        replay.replay()
+    ms = replay.ms_per_call(reps=3)
     a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
     for _ in range(4):
@@ -528,7 +503,7 @@ def profile_shape(torch, G, dev, name: str, M: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"profile": name, "shape": name, "M": M, "config": op.resolved_config,
                       "kernel": KERNEL_NAMES[op.resolved_config["kernel"]], "us_per_launch": round(ms * 1000, 3),
-                      "algorithmic_bytes": algo_bytes(name, M), "launches": len(calls) * 14,
+                      "algorithmic_bytes": algo_bytes(name, M), "launches": len(calls) * 12 + 3,
                       "copy_bytes": 256 << 20, "copies": 4}), flush=True)
     return 0
 

@@ -150,6 +150,16 @@ size_t krk_gemm_config_workspace_bytes(int M, int N, int K, int epilogue,
                                        const krk_gemm_config* cfg);
 
 /*
+ * krk_gemm_resolve — the configuration krk_gemm_bf16_config runs for `cfg`
+ * (0 fields filled from krk_gemm_plan; NULL = the plan itself), or
+ * KRK_ERR_UNSUPPORTED / KRK_ERR_INVALID with krk_last_error() explaining why
+ * this build cannot run it.  The check the reference's constructors make
+ * before a launch (SkinnyMatmul / SkinnyGateUp / Gemv.__init__,
+ * engine/kernels/gemm.py:251-254, 301-311, 333-344), without launching.
+ */
+int krk_gemm_resolve(int M, int N, int K, int epilogue, const krk_gemm_config* cfg, krk_gemm_config* out);
+
+/*
  * krk_gemm_bf16_config — krk_gemm_bf16 with an explicit configuration, the
  * counterpart of calling one candidate SkinnyMatmul(M, N, K, device, **cfg)
  * (engine/kernels/gemm.py:427-448).  Every configuration computes the same

@@ -363,6 +363,11 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
             return fail(KRK_ERR_INVALID, "m_tiles=%d cannot cover %d rows (need %d..4)", c.m_tiles, Mc, cdiv(Mc, 16));
         if (c.splits < 1 || c.splits > 32)
             return fail(KRK_ERR_UNSUPPORTED, "splits=%d not in 1..32", c.splits);
+        // Every split must own at least one K stage: a workgroup of an empty
+        // split would not take part in its blocks' fix-up.
+        if (c.splits > cdiv(K, krk::kStreamKC))
+            return fail(KRK_ERR_UNSUPPORTED, "STREAM splits=%d exceeds the %d K stages of %d elements", c.splits,
+                        cdiv(K, krk::kStreamKC), krk::kStreamKC);
         if (stream_xs(c.m_tiles, cdiv(cdiv(K, krk::kStreamKC), c.splits)) == 0)
             return fail(KRK_ERR_UNSUPPORTED, "STREAM keeps x in registers: %d K stages per split x %d m tiles is too "
                         "many (raise splits)", cdiv(cdiv(K, krk::kStreamKC), c.splits), c.m_tiles);
@@ -765,9 +770,13 @@ WorkspaceLayout workspace_layout(int M, int N, int K, int epilogue, const krk_ge
     return l;
 }
 
+// fixed_part_off: 0 for the caller-sized workspace layout; otherwise the
+// split-K partials start at this offset and the counters of every call share
+// the region before it.
 int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
               int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
-              void* workspace, size_t workspace_bytes, void* stream, const NormSpec* ns = nullptr) {
+              void* workspace, size_t workspace_bytes, void* stream, const NormSpec* ns = nullptr,
+              size_t fixed_part_off = 0) {
     g_err[0] = '\0';
     int rc = check_shape(M, N, K, epilogue);
     if (rc) return rc;
@@ -833,9 +842,8 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
 
     const Geometry g = geometry(M, N, epilogue, c);
     uint32_t* ctr = wl.gemm ? static_cast<uint32_t*>(workspace) : nullptr;
-    float* part = wl.gemm ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                     align_up((size_t)g.nblocks * sizeof(uint32_t), 256))
-                          : nullptr;
+    const size_t part_off = fixed_part_off ? fixed_part_off : align_up((size_t)g.nblocks * sizeof(uint32_t), 256);
+    float* part = wl.gemm ? reinterpret_cast<float*>(static_cast<char*>(workspace) + part_off) : nullptr;
     hipStream_t st = static_cast<hipStream_t>(stream);
     krk::NormArgs na{};
     if (ns) na = krk::NormArgs{static_cast<const uint16_t*>(ns->d), ns->ldd, static_cast<const uint16_t*>(ns->w_norm),
@@ -1237,6 +1245,14 @@ size_t krk_gemm_config_workspace_bytes(int M, int N, int K, int epilogue, const 
     krk_gemm_config c;
     if (resolve_config(M, N, K, epilogue, cfg, &c)) return 0;
     return workspace_for(M, N, epilogue, c);
+}
+
+int krk_gemm_resolve(int M, int N, int K, int epilogue, const krk_gemm_config* cfg, krk_gemm_config* out) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    if (!out) return fail(KRK_ERR_INVALID, "null output config");
+    return resolve_config(M, N, K, epilogue, cfg, out);
 }
 
 int krk_gemm_plan(int M, int N, int K, int epilogue, krk_gemm_config* out) {

@@ -72,6 +72,7 @@ SIGNATURES = {
     "krk_gemm_workspace_bytes": (_size, [_int, _int, _int, _int]),
     "krk_gemm_plan": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_gemm_config_workspace_bytes": (_size, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_resolve": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig), ctypes.POINTER(GemmConfig)]),
     "krk_gemm_bf16_config": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
                                      _int, _int, _int, _int, ctypes.POINTER(GemmConfig),
                                      _c_void_p, _size, _c_void_p]),

@@ -31,12 +31,12 @@ import ctypes
 import torch
 import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, timing
 from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "SkinnySelect", "pick_matmul", "pick_gateup", "pick_normed",
-    "add_rms_norm", "plan", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
+    "add_rms_norm", "plan", "resolve", "config_from_triton", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
 ]
 
 
@@ -170,25 +170,116 @@ def add_rms_norm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, eps: fl
     return out
 
 
+_TRITON_KEYS = ("block_n", "block_k", "split_k", "num_warps", "num_stages")
+
+
+def _largest_at_most(v: int, allowed) -> int:
+    fit = [a for a in allowed if a <= v]
+    return max(fit) if fit else min(allowed)
+
+
+def resolve(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE, config: dict | None = None) -> dict:
+    """The configuration the library runs for ``config`` (0 or missing fields
+    from the dispatch table); ValueError if this build cannot run it."""
+    cfg = GemmConfig.from_dict(config) if config is not None else None
+    out = GemmConfig()
+    _lib.check(_lib.load().krk_gemm_resolve(M, N, K, epilogue, ctypes.byref(cfg) if cfg else None, ctypes.byref(out)))
+    return out.as_dict()
+
+
+def config_from_triton(M: int, N: int, K: int, epilogue: int, block_n: int, block_k: int, split_k: int,
+                       num_warps: int, num_stages: int, persist: int = 0) -> dict:
+    """Translate the reference's Triton constructor arguments
+    (``SkinnyMatmul / SkinnyGateUp(M, N, K, device, block_n, block_k, split_k,
+    num_warps, num_stages, persist)``, ``Gemv(...)``; engine/kernels/gemm.py:251,
+    301, 333 and the CONFIGS / GEMV_CONFIGS lists at :284-288, 364-375) into
+    the nearest configuration this library instantiates.  The split count and
+    the persistent grid carry over; tile sizes map onto the kernel that serves
+    the row count:
+
+    * ``persist > 0``: the persistent stream kernel with ``split_k`` K splits,
+      raised where needed until each split's K range fits its x registers;
+    * at most 8 rows per launch: the VALU kernel with ``num_warps`` waves
+      (1, 2, 4 or 8) and ``block_n / num_warps`` W rows per wave (1, 2 or 4);
+    * otherwise the LDS-staged MFMA kernel with ``block_n / 16`` W tiles
+      (1, 2 or 4), three stages in flight when ``num_stages >= 4``, 512-k
+      stages when ``block_k >= 512``.
+
+    SILU_MUL needs an even number of W rows per wave or tile (gate and up).
+    Raises ValueError when the library cannot run the result."""
+    for name, v in (("block_n", block_n), ("block_k", block_k), ("split_k", split_k), ("num_warps", num_warps),
+                    ("num_stages", num_stages)):
+        if not isinstance(v, int) or v < 1:
+            raise ValueError(f"{name} must be a positive int, got {v!r}")
+    silu = epilogue == EPILOGUE_SILU_MUL
+    rows = min(M, 64)
+    splits = min(split_k, 32)
+    if persist:
+        cfg = {"kernel": _lib.KERNEL_STREAM, "splits": splits}
+    elif rows <= 8:
+        waves = _largest_at_most(num_warps, (1, 2, 4, 8))
+        per_wave = _largest_at_most(max(1, block_n // waves), (2, 4) if silu else (1, 2, 4))
+        cfg = {"kernel": _lib.KERNEL_VALU, "waves": waves, "n_tiles": per_wave,
+               "splits": min(splits, -(-K // 512))}
+    else:
+        tiles = _largest_at_most(max(1, block_n // 16), (2, 4) if silu else (1, 2, 4))
+        cfg = {"kernel": _lib.KERNEL_MFMA_LDS, "n_tiles": tiles, "unroll": 3 if num_stages >= 4 else 2,
+               "k_chunk": 512 if block_k >= 512 else 256, "splits": splits}
+    if persist:
+        for sp in range(splits, 33):
+            try:
+                return resolve(M, N, K, epilogue, dict(cfg, splits=sp))
+            except ValueError:
+                if sp == 32:
+                    raise
+    try:
+        return resolve(M, N, K, epilogue, cfg)
+    except ValueError:
+        if cfg.get("unroll") == 3:  # three stages in flight exist only for small tiles
+            cfg["unroll"] = 2
+            return resolve(M, N, K, epilogue, cfg)
+        raise
+
+
+def _constructor_config(M, N, K, epilogue, config, triton_args: dict, persist: int) -> dict | None:
+    given = {k: v for k, v in triton_args.items() if v is not None}
+    if not given and not persist:
+        return dict(config) if config else None
+    if config:
+        raise ValueError("give either config= or the reference's Triton arguments, not both")
+    missing = [k for k in _TRITON_KEYS if k not in given]
+    if missing:
+        raise ValueError(f"the reference's constructor arguments come together; missing {', '.join(missing)}")
+    return config_from_triton(M, N, K, epilogue, persist=persist, **given)
+
+
 class SkinnyMatmul:
     """``c = a @ w.T`` for a fixed (M, N, K): bf16 in, fp32 accumulation, bf16 out.
 
     Mirrors the reference's ``SkinnyMatmul`` (engine/kernels/gemm.py:332-361):
     the split-K workspace belongs to the object and is allocated (zero-filled)
-    once here; each call allocates only its output.  ``config`` optionally
-    forces a kernel configuration (keys of ``krk_gemm_config``).
+    once here; each call allocates only its output.  It is built like the
+    reference's, ``SkinnyMatmul(M, N, K, device, block_n, block_k, split_k,
+    num_warps, num_stages, persist=0)`` (the Triton tile arguments are
+    translated by :func:`config_from_triton`), or with ``config=`` (keys of
+    ``krk_gemm_config``), or with neither (the dispatch table's plan).  A
+    configuration this build cannot run raises ValueError here.
     """
 
     epilogue = EPILOGUE_NONE
 
-    def __init__(self, M: int, N: int, K: int, device, config: dict | None = None):
+    def __init__(self, M: int, N: int, K: int, device, block_n: int | None = None, block_k: int | None = None,
+                 split_k: int | None = None, num_warps: int | None = None, num_stages: int | None = None,
+                 persist: int = 0, *, config: dict | None = None):
         if M < 1 or N < 1 or K < 8 or K % 8:
             raise ValueError(f"unsupported shape M={M} N={N} K={K} (need K >= 8, K % 8 == 0)")
         self.M, self.N, self.K = M, N, K
         self.device = torch.device(device)
-        self.config = dict(config) if config else None
-        # An invalid explicit config also reports 0 here; the first call then
-        # raises ValueError with the library's explanation.
+        triton_args = dict(block_n=block_n, block_k=block_k, split_k=split_k, num_warps=num_warps,
+                           num_stages=num_stages)
+        self.config = _constructor_config(M, N, K, self.epilogue, config, triton_args, persist)
+        if self.config is not None:
+            resolve(M, N, K, self.epilogue, self.config)  # ValueError now, not at the first call
         # One workspace serves plain and normed calls: both keep their split-K
         # counters at its start; normed calls may use more of it as scratch.
         nbytes = max(workspace_bytes(M, N, K, self.epilogue, self.config),
@@ -198,9 +289,7 @@ class SkinnyMatmul:
 
     @property
     def resolved_config(self) -> dict:
-        if self.config is None:
-            return plan(self.M, self.N, self.K, self.epilogue)
-        return dict(self.config)
+        return resolve(self.M, self.N, self.K, self.epilogue, self.config)
 
     def run(self, a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, norm=None) -> torch.Tensor:
         """Allocation-free form: write into ``out``."""
@@ -221,16 +310,22 @@ class SkinnyGateUp(SkinnyMatmul):
 
     ``I`` is the intermediate width; the weight is ``[2*I, K]`` with the gate
     rows first (engine/model.py:116).  Rounding follows the reference's three
-    bf16 boundaries (engine/kernels/gemm.py:107-113).  Call as ``f(a, wgu)`` or,
-    like the reference (engine/kernels/gemm.py:314), ``f(a, wg, wu)`` with
-    ``wg = wgu[:I]`` and ``wu = wgu[I:]`` views of one tensor.
+    bf16 boundaries (engine/kernels/gemm.py:107-113).  Built like the
+    reference's ``SkinnyGateUp(M, I, K, device, block_n, block_k, split_k,
+    num_warps, num_stages, persist=0)`` (gemm.py:301) or with ``config=``.
+    Call as ``f(a, wgu)`` or, like the reference (engine/kernels/gemm.py:314),
+    ``f(a, wg, wu)`` with ``wg = wgu[:I]`` and ``wu = wgu[I:]`` views of one
+    tensor.
     """
 
     epilogue = EPILOGUE_SILU_MUL
 
-    def __init__(self, M: int, I: int, K: int, device, config: dict | None = None):
+    def __init__(self, M: int, I: int, K: int, device, block_n: int | None = None, block_k: int | None = None,
+                 split_k: int | None = None, num_warps: int | None = None, num_stages: int | None = None,
+                 persist: int = 0, *, config: dict | None = None):
         self.I = I
-        super().__init__(M, 2 * I, K, device, config)
+        super().__init__(M, 2 * I, K, device, block_n, block_k, split_k, num_warps, num_stages, persist,
+                         config=config)
 
     def __call__(self, a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor | None = None, norm=None) -> torch.Tensor:
         wgu = wg if wu is None else _join_halves(wg, wu, self.I)
@@ -248,67 +343,52 @@ def _join_halves(wg: torch.Tensor, wu: torch.Tensor, I: int) -> torch.Tensor:
 
 
 class Gemv(SkinnyMatmul):
-    """M = 1 row dot products (reference ``Gemv``, engine/kernels/gemm.py:248-281).
-    ``gateup=True`` applies the SwiGLU epilogue like the reference's GATEUP mode."""
+    """Row dot products for at most 4 rows (reference ``Gemv``,
+    engine/kernels/gemm.py:248-281), built like the reference's ``Gemv(M, N, K,
+    device, block_n, block_k, split_k, num_warps, num_stages, gateup=False)``
+    or with ``config=``.  ``N`` is the output width; ``gateup=True`` applies
+    the SwiGLU epilogue like the reference's GATEUP mode, with the gate and up
+    weights passed as ``f(a, wg, wu)`` (halves of one ``[2N, K]`` weight) or
+    ``f(a, wgu)``."""
 
-    def __init__(self, M: int, N: int, K: int, device, gateup: bool = False, config: dict | None = None):
+    def __init__(self, M: int, N: int, K: int, device, block_n: int | None = None, block_k: int | None = None,
+                 split_k: int | None = None, num_warps: int | None = None, num_stages: int | None = None,
+                 gateup: bool = False, *, config: dict | None = None):
         if M > 4:
             raise ValueError("Gemv handles at most 4 rows")
         self.epilogue = EPILOGUE_SILU_MUL if gateup else EPILOGUE_NONE
-        super().__init__(M, 2 * N if gateup else N, K, device, config)
         self.I = N
+        super().__init__(M, 2 * N if gateup else N, K, device, block_n, block_k, split_k, num_warps, num_stages,
+                         config=config)
 
     def __call__(self, a: torch.Tensor, w: torch.Tensor, w2: torch.Tensor | None = None, norm=None) -> torch.Tensor:
-        if self.epilogue == EPILOGUE_SILU_MUL:
-            w = w if w2 is None else _join_halves(w, w2, self.I)
+        if self.epilogue == EPILOGUE_SILU_MUL and w2 is not None:
+            w = _join_halves(w, w2, self.I)
+        elif w2 is not None:
+            raise ValueError("a second weight is only taken with gateup=True")
         return super().__call__(a, w, norm)
 
 
 def _time(fn, iters: int = 30, rotate: list | None = None) -> float:
-    """Average milliseconds per call, measured as a graph replay.
-
-    Same method as the reference (engine/kernels/gemm.py:378-414): 3 warm-up
-    calls on a side stream, ``iters`` calls captured in one graph (rotating
-    over ``rotate`` so consecutive calls stream distinct weights), the median
-    of 5 timed replays divided by ``iters``.
-    """
-    ws = rotate or [None]
-    call = (lambda i: fn(ws[i % len(ws)])) if rotate else (lambda i: fn())
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for i in range(3):
-            call(i)
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(iters):
-            call(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    samples = []
-    for _ in range(5):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        samples.append(start.elapsed_time(end) / iters)
-    samples.sort()
-    return samples[len(samples) // 2]
+    """Milliseconds per call of ``fn`` (``fn(w)`` over the weights of
+    ``rotate`` in turn, else ``fn()``), ``iters`` calls replayed from one
+    graph: the reference picker timer's signature
+    (engine/kernels/gemm.py:378-414) over :mod:`kernels.timing`."""
+    return timing.replay_ms(timing.rotation_calls(fn, iters, rotate))
 
 
 def _validate(out: torch.Tensor, ref: torch.Tensor, what: str, log=None) -> None:
-    """Reference acceptance rule (engine/kernels/gemm.py:441-447): max error
-    within ``0.02 * max|ref| + 1e-3``.  A failure raises instead of falling back."""
-    out, ref = out.float(), ref.float()
-    err = (out - ref).abs().max().item()
-    tol = 0.02 * ref.abs().max().item() + 1e-3
-    if not (err <= tol):
-        raise RuntimeError(f"{what}: HIP GEMM disagrees with F.linear (err {err:.4g} > tol {tol:.4g})")
+    """The tuner's acceptance (:func:`kernels.tune.close_ok`): every element
+    within ``2e-2 + 1e-2·|ref|`` and the reference's rule
+    (engine/kernels/gemm.py:441-447), max error within ``0.02 * max|ref| + 1e-3``.
+    A failure raises instead of falling back."""
+    from . import tune
+
+    ok, why = tune.close_ok(out, ref)
+    if not ok:
+        raise RuntimeError(f"{what}: HIP GEMM disagrees with F.linear ({why})")
     if log:
-        log(f"{what}: validated (err {err:.3g} <= {tol:.3g})")
+        log(f"{what}: validated ({why})")
 
 
 def _linear_fp32acc(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -328,8 +408,8 @@ def _silu_mul(gu: torch.Tensor) -> torch.Tensor:
 
 def _projection(M: int, N: int, K: int, epilogue: int, device, config: dict | None) -> SkinnyMatmul:
     if epilogue == EPILOGUE_SILU_MUL:
-        return SkinnyGateUp(M, N // 2, K, device, config)
-    return SkinnyMatmul(M, N, K, device, config)
+        return SkinnyGateUp(M, N // 2, K, device, config=config)
+    return SkinnyMatmul(M, N, K, device, config=config)
 
 
 def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_NONE, ws: list | None = None,
@@ -346,22 +426,32 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
     rot = ws or [w]
     cache = tune.default_cache() if cache is None else cache
     kind = "gateup" if epilogue == EPILOGUE_SILU_MUL else "matmul"
+    # Candidates are validated on the call's weight and on a second one of
+    # the rotation, each against its own fp32-accumulated torch result.
+    checks = [w] + [v for v in rot[1:2] if v is not w]
+
+    def project(inp, weight):
+        ref = _linear_fp32acc(inp, weight)
+        return _silu_mul(ref) if epilogue == EPILOGUE_SILU_MUL else ref
+
     if norm is None:
-        ref = _linear_fp32acc(a, w)
-        ref = _silu_mul(ref) if epilogue == EPILOGUE_SILU_MUL else ref
+        refs = [project(a, v) for v in checks]
 
         def build(cfg):
             mm = _projection(M, N, K, epilogue, a.device, cfg)
             return lambda w_: mm(a, w_)
 
         def accept(fn):
-            return tune.max_err_ok(fn(w), ref)
+            for v, ref in zip(checks, refs):
+                ok, why = tune.close_ok(fn(v), ref)
+                if not ok:
+                    return ok, why
+            return ok, why
     else:
         y, w_norm, eps = norm
         kind = "normed-" + kind
         ref_xout, n = _add_rms_norm_ref(a, y, w_norm, eps)
-        ref = _linear_fp32acc(n, w)
-        ref = _silu_mul(ref) if epilogue == EPILOGUE_SILU_MUL else ref
+        refs = [project(n, v) for v in checks]
         xout = torch.empty_like(a)
 
         def build(cfg):
@@ -369,11 +459,15 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
             return lambda w_: mm(a, w_, norm=(y, w_norm, xout, eps))
 
         def accept(fn):
-            xout.fill_(0)
-            out = fn(w)
-            if not torch.equal(xout, ref_xout):
-                return False, "xout differs from x + y"
-            return tune.max_err_ok(out, ref)
+            for v, ref in zip(checks, refs):
+                xout.fill_(0)
+                out = fn(v)
+                if not torch.equal(xout, ref_xout):
+                    return False, "xout differs from x + y"
+                ok, why = tune.close_ok(out, ref)
+                if not ok:
+                    return ok, why
+            return ok, why
     timer = lambda fn, rot_: _time(fn, rotate=rot_)
     return tune.search(kind, M, N, K, epilogue, a.device, build, accept, timer, rot, log=log, cache=cache, limit=limit)
 
@@ -388,7 +482,7 @@ def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = No
     M, K = a.shape
     N = w.shape[0]
     cfg = tune_projection(a, w, EPILOGUE_NONE, ws, log, cache).config if tune else None
-    mm = SkinnyMatmul(M, N, K, a.device, cfg)
+    mm = SkinnyMatmul(M, N, K, a.device, config=cfg)
     _validate(mm(a, w), _linear_fp32acc(a, w), f"matmul M={M} N={N} K={K}", log)
     if log:
         ms = _time(lambda w_: mm(a, w_), rotate=ws or [w])
@@ -404,7 +498,7 @@ def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = 
     M, K = a.shape
     I = wgu.shape[0] // 2
     cfg = tune_projection(a, wgu, EPILOGUE_SILU_MUL, ws, log, cache).config if tune else None
-    mm = SkinnyGateUp(M, I, K, a.device, cfg)
+    mm = SkinnyGateUp(M, I, K, a.device, config=cfg)
     _validate(mm(a, wgu), _silu_mul(_linear_fp32acc(a, wgu)), f"gateup M={M} I={I} K={K}", log)
     if log:
         ms = _time(lambda w_: mm(a, w_), rotate=ws or [wgu])

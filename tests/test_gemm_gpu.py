@@ -36,7 +36,9 @@ def krk(x, w, epilogue=NONE, config=None, device="cuda:0"):
     xd, wd = x.to(device), w.to(device)
     M, N = x.shape[0], w.shape[0]
     nout = N // 2 if epilogue == SILU else N
-    y = torch.empty((M, nout), dtype=torch.bfloat16, device=device)
+    # NaN-filled, so an output the kernel fails to write cannot pass by
+    # holding a previous call's correct result (torch's allocator reuses blocks)
+    y = torch.full((M, nout), float("nan"), dtype=torch.bfloat16, device=device)
     nbytes = G.workspace_bytes(M, N, x.shape[1], epilogue, config)
     ws = torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes else None
     G.gemm_into(xd, wd, y, epilogue, ws, config)
@@ -153,22 +155,32 @@ def test_lm_head_argmax(device, lm_head, M):
     _lm_argmax_check(x, lm_head, f"lm_head M={M}", device)
 
 
-@pytest.mark.parametrize("layer", [0, 17, 35])
+@pytest.mark.parametrize("layer", range(R.LAYERS))
 def test_c4_sweep_layers_m32(device, layer):
-    """C4: M=32 through one layer's four projections (teacher-forced: each
-    GEMM is fed the oracle's input, so bf16 differences do not compound)."""
+    """C4: M=32 through every layer's four projections, each layer with its
+    own seeded weights (teacher-forced: each GEMM is fed the oracle's input,
+    so bf16 differences do not compound).  Layers 0, 17 and 35 also get the
+    fp64 rounding check."""
     M = 32
+    check = check_linear if layer in (0, 17, 35) else _check_linear_parity
     h = R.randn_bf16((M, R.HIDDEN), R.seed_for(4, layer, "x"))
     wqkv = R.randn_bf16((6144, R.HIDDEN), R.seed_for(4, layer, "qkv"), 0.02)
     wo = R.randn_bf16((R.HIDDEN, R.Q_WIDTH), R.seed_for(4, layer, "o"), 0.02)
     wgu = R.randn_bf16((2 * R.INTER, R.HIDDEN), R.seed_for(4, layer, "gate_up"), 0.02)
     wd = R.randn_bf16((R.HIDDEN, R.INTER), R.seed_for(4, layer, "down"), 0.02)
-    qkv = check_linear(h, wqkv, f"C4 L{layer} qkv")
+    qkv = check(h, wqkv, f"C4 L{layer} qkv")
     attn = R.linear_bf16(h, wqkv)[:, :R.Q_WIDTH].contiguous()  # stand-in attention output
-    check_linear(attn, wo, f"C4 L{layer} o")
+    check(attn, wo, f"C4 L{layer} o")
     act = check_gateup(h, wgu, f"C4 L{layer} gate_up")
-    check_linear(R.gateup_bf16(h, wgu), wd, f"C4 L{layer} down")
+    check(R.gateup_bf16(h, wgu), wd, f"C4 L{layer} down")
     assert qkv.shape == (M, 6144) and act.shape == (M, R.INTER)
+
+
+def _check_linear_parity(x, w, what, config=None):
+    say(what, tuple(x.shape), tuple(w.shape), config)
+    y = krk(x, w, NONE, config)
+    assert_parity(y, R.linear_bf16(x, w), what)
+    return y
 
 
 # ---------------------------------------------------------------- edge cases
@@ -263,6 +275,86 @@ def test_special_inputs_exact(device):
         assert torch.equal(y[r], w[:, c]), f"one-hot row {r} (k={c}) wrong"
     y2 = krk(-oh, w)
     assert torch.equal(y2, -y)
+
+
+# One configuration of every kernel family, with and without split K.
+SPECIAL_FAMILIES = [
+    ("valu", 4, dict(kernel=_lib.KERNEL_VALU, splits=1)),
+    ("valu split-K", 3, dict(kernel=_lib.KERNEL_VALU, splits=3)),
+    ("valu x in registers", 2, dict(kernel=_lib.KERNEL_VALU, splits=2)),
+    ("lds-staged", 16, dict(kernel=_lib.KERNEL_MFMA_LDS, splits=1)),
+    ("lds-staged split-K", 24, dict(kernel=_lib.KERNEL_MFMA_LDS, splits=3)),
+    ("stream", 33, dict(kernel=_lib.KERNEL_STREAM, splits=1)),
+    ("stream split-K", 8, dict(kernel=_lib.KERNEL_STREAM, splits=2)),
+    ("register mfma split-K", 13, dict(kernel=_lib.KERNEL_MFMA, splits=2)),
+]
+
+
+def _special_operands(M, N, K, seed):
+    """Random operands with NaN, +-inf and -0 planted in x rows and W rows.
+    x: row 0 NaN at one k; row 1 +inf; row 2 -inf and +inf (products of
+    either sign: NaN or an infinity per channel); row 3 all -0.  W: channel 3
+    NaN; channel 5 +inf; channel 6 -inf; channel 9 all -0; channel 10 +inf at
+    the k where x row 1 is +inf."""
+    x = R.randn_bf16((M, K), seed)
+    w = R.randn_bf16((N, K), seed + 1, 0.02)
+    inf, nan = float("inf"), float("nan")
+    x[0, 5] = nan
+    x[min(1, M - 1), 17] = inf
+    if M > 2:
+        x[2, K // 3] = -inf
+        x[2, K - 1] = inf
+    if M > 3:
+        x[3, :] = -0.0
+    w[3, 7] = nan
+    w[5, K // 2] = inf
+    w[6, 1] = -inf
+    w[9, :] = -0.0
+    w[10, 17] = inf
+    return x, w
+
+
+def _assert_special_parity(y, ref, what):
+    """NaN exactly where the oracle has NaN, infinities equal (with sign),
+    every finite value within the north-star tolerance.  (The sign of a zero
+    result depends on the summation order and is not compared: -0 == +0.)"""
+    nan_y, nan_r = y.float().isnan(), ref.float().isnan()
+    assert torch.equal(nan_y, nan_r), f"{what}: NaN mask differs at {(nan_y != nan_r).nonzero()[:6].tolist()}"
+    inf_r = ref.float().isinf()
+    assert torch.equal(y.float().isinf(), inf_r), f"{what}: infinity mask differs"
+    assert torch.equal(y.float()[inf_r], ref.float()[inf_r]), f"{what}: infinity signs differ"
+    fin = ~(nan_r | inf_r)
+    yf, rf = y.float()[fin], ref.float()[fin]
+    bad = (yf - rf).abs() > 2e-2 + 1e-2 * rf.abs()
+    assert not bad.any(), f"{what}: {int(bad.sum())} finite values outside 2e-2 + 1e-2|ref|"
+
+
+@pytest.mark.parametrize("family,M,config", SPECIAL_FAMILIES, ids=[f[0] for f in SPECIAL_FAMILIES])
+@pytest.mark.parametrize("epi", [NONE, SILU], ids=["plain", "silu_mul"])
+def test_special_values_propagate(device, family, M, config, epi):
+    """NaN, +-inf and -0 in x and in W rows, through every kernel family
+    (VALU dot2, LDS-staged MFMA, stream MFMA, register MFMA), the split-K
+    fix-up and the SiLU*mul epilogue (expf at +-inf), against F.linear /
+    swiglu on the CPU."""
+    K = 2048
+    N = 64 if epi == NONE else 96
+    x, w = _special_operands(M, N, K, 9100 + M)
+    if epi == SILU:
+        # gate rows 0..47, up rows 48..95: put specials in gate and up rows
+        w[48 + 3, 11] = float("nan")   # up row of channel 3 (gate row 3 is NaN too)
+        w[48 + 20, 17] = -float("inf")  # up row of channel 20: x row 1 gives -inf * +inf
+        w[30, 17] = -float("inf")      # gate row of channel 30 at x row 1's +inf: silu(-inf)
+    cfg = dict(config)
+    say("special values", family, "M", M, "epi", epi, cfg)
+    y = krk(x, w, epi, cfg)
+    ref = R.gateup_bf16(x, w) if epi == SILU else R.linear_bf16(x, w)
+    # the planted values do reach the outputs
+    assert ref.float().isnan().any() and ref.float().isinf().any()
+    _assert_special_parity(y, ref, f"{family} {'silu' if epi == SILU else 'plain'}")
+    if epi == NONE and M > 3:
+        # rows from 3 on hold no NaN or infinity (row 3 is all -0)
+        assert (y[3:, 9].float() == 0).all(), "a -0 weight row gives zeros"
+        assert (y[3].float().nan_to_num(1.0) == 0).sum() == N - 4, "a -0 x row gives zeros (NaN at the 4 NaN/inf channels)"
 
 
 # ---------------------------------------------------------------- configurations
@@ -521,6 +613,56 @@ def test_pickers_return_validated_callables(device):
     assert any("us" in l for l in logs)
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_gemv_wrapper(device, M):
+    """Gemv (reference engine/kernels/gemm.py:248-281): plain; gateup=True
+    with the gate and up weights as the two halves of one tensor or as the
+    whole tensor; and every one of the reference's GEMV_CONFIGS
+    (gemm.py:284-288) through the Triton-argument constructor."""
+    K, N, I = 2560, 6144, 1216
+    x = R.randn_bf16((M, K), 9300 + M)
+    w = R.randn_bf16((N, K), 9301, 0.02)
+    wgu = R.randn_bf16((2 * I, K), 9302, 0.02)
+    xd, wd, wgud = x.to(device), w.to(device), wgu.to(device)
+    say("Gemv", M)
+    assert_parity(G.Gemv(M, N, K, device)(xd, wd).cpu(), R.linear_bf16(x, w), f"Gemv M={M}")
+    gu = G.Gemv(M, I, K, device, gateup=True)
+    halves = gu(xd, wgud[:I], wgud[I:]).cpu()
+    assert_parity(halves, R.gateup_bf16(x, wgu), f"Gemv gateup M={M}")
+    assert torch.equal(gu(xd, wgud).cpu(), halves)
+    with pytest.raises(ValueError):
+        gu(xd, wgud[:I], wgud[I:].clone())  # not the two halves of one weight
+    for cfg in ({"block_n": 32, "block_k": 256, "split_k": 1, "num_warps": 4, "num_stages": 3},
+                {"block_n": 32, "block_k": 256, "split_k": 4, "num_warps": 4, "num_stages": 3},
+                {"block_n": 16, "block_k": 256, "split_k": 8, "num_warps": 2, "num_stages": 3}):
+        say("Gemv reference config", cfg)
+        assert_parity(G.Gemv(M, N, K, device, **cfg)(xd, wd).cpu(), R.linear_bf16(x, w), f"Gemv {cfg}")
+        g2 = G.Gemv(M, I, K, device, gateup=True, **cfg)
+        assert_parity(g2(xd, wgud[:I], wgud[I:]).cpu(), R.gateup_bf16(x, wgu), f"Gemv gateup {cfg}")
+
+
+@pytest.mark.parametrize("M", [8, 16, 32])
+def test_reference_constructor_configs(device, M):
+    """SkinnyMatmul / SkinnyGateUp built from the reference's CONFIGS
+    (engine/kernels/gemm.py:364-375) run the translated configuration and
+    match the oracle."""
+    K, N, I = 2560, 768, 1216
+    x = R.randn_bf16((M, K), 9400 + M)
+    w = R.randn_bf16((N, K), 9401, 0.02)
+    wgu = R.randn_bf16((2 * I, K), 9402, 0.02)
+    xd, wd, wgud = x.to(device), w.to(device), wgu.to(device)
+    ref, ref_gu = R.linear_bf16(x, w), R.gateup_bf16(x, wgu)
+    for cfg in ({"block_n": 64, "block_k": 128, "split_k": 1, "num_warps": 4, "num_stages": 3},
+                {"block_n": 64, "block_k": 64, "split_k": 4, "num_warps": 4, "num_stages": 4},
+                {"block_n": 32, "block_k": 64, "split_k": 8, "num_warps": 4, "num_stages": 4},
+                {"block_n": 32, "block_k": 128, "split_k": 2, "num_warps": 4, "num_stages": 3, "persist": 2}):
+        mm = G.SkinnyMatmul(M, N, K, device, **cfg)
+        say("reference config", M, cfg, mm.resolved_config)
+        assert_parity(mm(xd, wd).cpu(), ref, f"SkinnyMatmul {cfg}")
+        gu = G.SkinnyGateUp(M, I, K, device, **cfg)
+        assert_parity(gu(xd, wgud[:I], wgud[I:]).cpu(), ref_gu, f"SkinnyGateUp {cfg}")
+
+
 # ------------------------------------------------------------------ warm-up tuner
 
 _TUNE_SHAPES = {"qkv": (2560, 6144, NONE), "o": (4096, 2560, NONE), "gate_up": (2560, 19456, SILU),
@@ -547,7 +689,7 @@ def test_tune_validates_every_candidate(device, shape, M):
     assert r.us <= r.plan_us
     again = G.tune_projection(a, ws[0], epi, ws=ws, cache=cache)
     assert again.cached and again.config == r.config
-    mm = G.SkinnyGateUp(M, N // 2, K, device, r.config) if epi == SILU else G.SkinnyMatmul(M, N, K, device, r.config)
+    mm = G.SkinnyGateUp(M, N // 2, K, device, config=r.config) if epi == SILU else G.SkinnyMatmul(M, N, K, device, config=r.config)
     ref = R.gateup_bf16(a.cpu(), ws[1].cpu()) if epi == SILU else R.linear_bf16(a.cpu(), ws[1].cpu())
     assert_parity(mm(a, ws[1]).cpu(), ref, f"tuned {shape} M={M}")
 

@@ -53,3 +53,168 @@ def test_cache_key_names_the_library_build(monkeypatch):
     tag = _lib.library_tag()
     assert len(tag) == 12 and tag == _lib.library_tag()
     assert TuneCache.key("cuda:0", "matmul", 1, 6144, 2560) == f"gfx950/{tag}/matmul/M1/N6144/K2560"
+
+
+class _EngineBudget:
+    """Stands in for the reference engine's ``budget`` module
+    (engine/budget.py: start / expired / remaining over one deadline)."""
+
+    def __init__(self, expired: bool):
+        self.is_expired = expired
+        self.started = []
+
+    def start(self, seconds):
+        self.started.append(seconds)
+
+    def expired(self):
+        return self.is_expired
+
+    def remaining(self):
+        return -1.0 if self.is_expired else 100.0
+
+
+def _search_with_stubs(monkeypatch, M=8, N=6144, K=2560):
+    """tune.search over the library's real candidate list with a fake build,
+    acceptance and timer: returns (result, configs that were timed)."""
+    from kernels import tune
+
+    timed = []
+
+    def build(cfg):
+        return lambda w: cfg
+
+    def accept(fn):
+        return True, "stub"
+
+    def timer(fn, rot):
+        cfg = fn(None)
+        timed.append(cfg)
+        return 1.0 + 0.01 * len(timed)
+
+    res = tune.search("matmul", M, N, K, 0, "cpu", build, accept, timer, [None], cache=None)
+    return res, timed
+
+
+def test_engine_budget_module_is_the_pickers_clock(monkeypatch):
+    """With the engine's ``budget`` module loaded and its deadline passed,
+    the tuner measures the dispatch table's plan and nothing else."""
+    import sys
+
+    from kernels import budget, tune
+
+    budget.use(None)
+    engine = _EngineBudget(expired=True)
+    monkeypatch.setitem(sys.modules, "budget", engine)
+    assert budget.shared() is engine and budget.expired() and budget.remaining() < 0
+    res, timed = _search_with_stubs(monkeypatch)
+    assert timed == [tune.candidates(8, 6144, 2560, 0)[0]]
+    assert res.config == timed[0] and res.plan_us is not None and len(res.trials) == 1
+    # start() goes to the engine's clock, not a private one
+    budget.start(7.0)
+    assert engine.started == [7.0]
+
+
+def test_open_engine_budget_lets_every_candidate_run(monkeypatch):
+    import sys
+
+    from kernels import budget, tune
+
+    budget.use(None)
+    monkeypatch.setitem(sys.modules, "budget", _EngineBudget(expired=False))
+    res, timed = _search_with_stubs(monkeypatch)
+    assert timed == tune.candidates(8, 6144, 2560, 0) and len(timed) > 10
+
+
+def test_explicit_budget_binding_wins(monkeypatch):
+    import sys
+
+    from kernels import budget
+
+    monkeypatch.setitem(sys.modules, "budget", _EngineBudget(expired=False))
+    mine = _EngineBudget(expired=True)
+    budget.use(mine)
+    try:
+        assert budget.shared() is mine and budget.expired()
+        _, timed = _search_with_stubs(monkeypatch)
+        assert len(timed) == 1
+    finally:
+        budget.use(None)
+
+
+def test_private_deadline_without_an_engine(monkeypatch):
+    import sys
+
+    from kernels import budget
+
+    budget.use(None)
+    monkeypatch.delitem(sys.modules, "budget", raising=False)
+    assert budget.shared() is None
+    budget.start(-1.0)
+    try:
+        assert budget.expired()
+        _, timed = _search_with_stubs(monkeypatch)
+        assert len(timed) == 1
+    finally:
+        budget.clear()
+    assert not budget.expired()
+
+
+def test_cli_line_for_cached_and_untimed_results():
+    """A cache hit has no plan time (plan_us None); the CLI prints it
+    instead of failing on a None format."""
+    from kernels.tune import Result, _us_text
+
+    cfg = {"kernel": 2}
+    assert "cached" in _us_text(Result(cfg, float("nan"), None, cached=True))
+    assert "-" in _us_text(Result(cfg, 5.0, None))
+    assert "5.00" in _us_text(Result(cfg, 5.0, 6.0)) and "6.00" in _us_text(Result(cfg, 5.0, 6.0))
+
+
+def test_search_cache_hit_is_not_timed(monkeypatch):
+    from kernels import _lib, budget, tune
+
+    class Props:
+        gcnArchName = "gfx950"
+
+    monkeypatch.setattr(tune.torch.cuda, "get_device_properties", lambda dev: Props())
+    budget.use(None)
+    cache = tune.TuneCache()
+    calls = []
+    build = lambda cfg: (lambda w: cfg)
+    timer = lambda fn, rot: calls.append(fn(None)) or 2.0
+    first = tune.search("matmul", 4, 2560, 4096, 0, "cuda:0", build, lambda fn: (True, ""), timer, [None],
+                        cache=cache, limit=3)
+    n = len(calls)
+    again = tune.search("matmul", 4, 2560, 4096, 0, "cuda:0", build, lambda fn: (True, ""), timer, [None],
+                        cache=cache, limit=3)
+    assert len(calls) == n == 3 and again.cached and again.plan_us is None and again.config == first.config
+
+
+def test_acceptance_rule_is_elementwise():
+    """close_ok: |out - ref| <= 2e-2 + 1e-2|ref| at every element, NaN and
+    infinities where the reference has them, plus the reference's global
+    rule.  A wrong small-magnitude channel passes the global rule alone and
+    must fail here."""
+    import torch
+
+    from kernels.tune import close_ok
+
+    ref = torch.linspace(-4, 4, 64).reshape(2, 32).to(torch.bfloat16)
+    assert close_ok(ref.clone(), ref)[0]
+    bad = ref.clone()
+    bad[0, 15] = ref[0, 15] + 0.05            # within 0.02 * max|ref| + 1e-3 = 0.081
+    ok_global = (bad.float() - ref.float()).abs().max() <= 0.02 * ref.float().abs().max() + 1e-3
+    assert ok_global and not close_ok(bad, ref)[0]
+    nan_ref = ref.clone()
+    nan_ref[1, 3] = float("nan")
+    assert not close_ok(ref, nan_ref)[0]
+    out = ref.clone()
+    out[1, 3] = float("nan")
+    assert close_ok(out, nan_ref)[0]
+    inf_ref = ref.clone()
+    inf_ref[0, 0] = float("inf")
+    out = ref.clone()
+    out[0, 0] = float("-inf")
+    assert not close_ok(out, inf_ref)[0]
+    out[0, 0] = float("inf")
+    assert close_ok(out, inf_ref)[0]
