@@ -290,6 +290,31 @@ int krk_gemm_select_plan(int M, int N, int K, int k, krk_gemm_config* out);
 int krk_gemm_select_fused(int M, int N, int K, int k, const krk_gemm_config* cfg);
 
 /*
+ * krk_gemm_bf16_noalloc — krk_gemm_bf16 without a workspace argument, for
+ * callers that cannot allocate device memory (code under HIP graph capture
+ * that may not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference: its kernels allocate their
+ * split-K partials per object (engine/kernels/gemm.py:341).
+ *
+ * The split-K counters and partials live in a static device array of
+ * KRK_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends (counters in its first KRK_NOALLOC_COUNTER_BYTES).
+ * A plan whose partials or counters do not fit returns KRK_ERR_WORKSPACE
+ * (every Qwen3-4B projection plan at M <= 64 fits: at most 1.97 MB).  The
+ * call allocates nothing and never synchronises.  All calls on one GPU share
+ * that GPU's array: calls that may overlap in time on one GPU (different
+ * streams, or several host threads) race and must not be issued; calls
+ * ordered on one stream are fine.
+ */
+#define KRK_NOALLOC_SCRATCH_BYTES (4u << 20)
+#define KRK_NOALLOC_COUNTER_BYTES (64u << 10)
+int krk_gemm_bf16_noalloc(const void* x, int64_t ldx,
+                          const void* w, int64_t ldw,
+                          void* y, int64_t ldy,
+                          int M, int N, int K, int epilogue,
+                          void* stream);
+
+/*
  * krk_last_error — text of the last error raised on the calling thread by
  * any krk_* function ("" if none).  Stands in for the ValueError messages of
  * engine/kernels/gateup64.py:63-74 and engine/kernels/gemm.py:253-254.

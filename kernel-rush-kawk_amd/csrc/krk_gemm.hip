@@ -772,7 +772,7 @@ WorkspaceLayout workspace_layout(int M, int N, int K, int epilogue, const krk_ge
 
 // fixed_part_off: 0 for the caller-sized workspace layout; otherwise the
 // split-K partials start at this offset and the counters of every call share
-// the region before it.
+// the region before it (the allocation-free entry point's static scratch).
 int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
               int M, int N, int K, int epilogue, const krk_gemm_config* cfg,
               void* workspace, size_t workspace_bytes, void* stream, const NormSpec* ns = nullptr,
@@ -1112,6 +1112,54 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
     return KRK_OK;
 }
 
+// ------------------------------------------------------- allocation-free calls
+// krk_gemm_bf16_noalloc keeps its split-K workspace in this static device
+// array instead of a caller's buffer: counters in the first
+// KRK_NOALLOC_COUNTER_BYTES (each call's blocks use counters from index 0;
+// every call leaves the ones it used at zero), fp32 partials after them.  In
+// host code `scratch` names a host-side stand-in, never the device memory:
+// the device address comes from hipGetSymbolAddress, once per device.
+constexpr int kScratchMaxDevices = 64;
+std::atomic<uintptr_t> g_scratch[kScratchMaxDevices];
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[KRK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// The current device's copy of `scratch`.  The first call on a device looks
+// up its address and zeroes the counter region with a kernel on `stream`
+// (the array starts zeroed; the clear keeps that invariant independent of the
+// loader).
+int scratch_on_current_device(unsigned char** out, hipStream_t stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kScratchMaxDevices)
+        return fail(KRK_ERR_UNSUPPORTED, "device %d: the static scratch is tracked for devices 0..%d", dev,
+                    kScratchMaxDevices - 1);
+    uintptr_t p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void* sym = nullptr;
+        e = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+        uint32_t* ctr = static_cast<uint32_t*>(sym);
+        int n = (int)(KRK_NOALLOC_COUNTER_BYTES / sizeof(uint32_t));
+        void* args[] = {(void*)&ctr, (void*)&n};
+        e = hipLaunchKernel(reinterpret_cast<const void*>(&zero_words_kernel), dim3(16), dim3(256), args, 0, stream);
+        if (e != hipSuccess) return hip_status(e, "scratch counter clear launch");
+        p = reinterpret_cast<uintptr_t>(sym);
+        g_scratch[dev].store(p, std::memory_order_release);
+    }
+    *out = reinterpret_cast<unsigned char*>(p);
+    return KRK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1231,6 +1279,31 @@ int krk_gemm_select_fused(int M, int N, int K, int k, const krk_gemm_config* cfg
     SelectPlan p;
     if ((rc = select_plan_for(M, N, K, k, cfg, &p))) return rc;
     return p.fused ? 1 : 0;
+}
+
+int krk_gemm_bf16_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                          int M, int N, int K, int epilogue, void* stream) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    krk_gemm_config c;
+    auto_config(M, N, K, epilogue, &c);
+    if (c.splits > 1) {
+        const Geometry g = geometry(M, N, epilogue, c);
+        const size_t counters = (size_t)g.nblocks * sizeof(uint32_t);
+        const size_t partials = (size_t)c.splits * (size_t)g.Mc * (size_t)N * sizeof(float);
+        if (counters > KRK_NOALLOC_COUNTER_BYTES || partials > KRK_NOALLOC_SCRATCH_BYTES - KRK_NOALLOC_COUNTER_BYTES)
+            return fail(KRK_ERR_WORKSPACE,
+                        "M=%d N=%d K=%d: the plan splits K %d ways and needs %zu bytes of partials and %d counters; "
+                        "the static scratch holds %zu bytes of partials and %zu counters (use krk_gemm_bf16 with a "
+                        "workspace)", M, N, K, c.splits, partials, g.nblocks,
+                        (size_t)(KRK_NOALLOC_SCRATCH_BYTES - KRK_NOALLOC_COUNTER_BYTES),
+                        (size_t)(KRK_NOALLOC_COUNTER_BYTES / sizeof(uint32_t)));
+    }
+    unsigned char* s = nullptr;
+    if ((rc = scratch_on_current_device(&s, static_cast<hipStream_t>(stream)))) return rc;
+    return gemm_impl(x, ldx, w, ldw, y, ldy, M, N, K, epilogue, nullptr, s, KRK_NOALLOC_SCRATCH_BYTES, stream, nullptr,
+                     KRK_NOALLOC_COUNTER_BYTES);
 }
 
 size_t krk_gemm_workspace_bytes(int M, int N, int K, int epilogue) {

@@ -94,6 +94,8 @@ SIGNATURES = {
     "krk_gemm_select_workspace_bytes": (_size, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_gemm_select_plan": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_gemm_select_fused": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_bf16_noalloc": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
+                                      _int, _int, _int, _int, _c_void_p]),
     "krk_gemm_candidates": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig), _int]),
     "krk_last_error": (ctypes.c_char_p, []),
 }

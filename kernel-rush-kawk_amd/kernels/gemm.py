@@ -36,7 +36,7 @@ from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "SkinnySelect", "pick_matmul", "pick_gateup", "pick_normed",
-    "add_rms_norm", "plan", "resolve", "config_from_triton", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
+    "add_rms_norm", "gemm_noalloc", "plan", "resolve", "config_from_triton", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
 ]
 
 
@@ -125,6 +125,28 @@ def gemm_into(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, epilogue: int =
         else:
             rc = lib.krk_gemm_bf16_config(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
                                           y.stride(0), M, N, K, epilogue, ctypes.byref(cfg), ws_ptr, ws_bytes, stream)
+    _lib.check(rc)
+    return y
+
+
+def gemm_noalloc(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, epilogue: int = EPILOGUE_NONE) -> torch.Tensor:
+    """``y = epilogue(x @ w.T)`` through ``krk_gemm_bf16_noalloc``: no
+    workspace argument and no allocation of any kind, for callers that cannot
+    allocate (code under graph capture, tight serving loops).  Split-K plans
+    use the library's static per-GPU scratch (``KRK_NOALLOC_SCRATCH_BYTES``);
+    a plan that does not fit raises ValueError.  Calls that may overlap in
+    time on one GPU share that scratch and must not be issued."""
+    M, K = x.shape
+    N = w.shape[0]
+    _check_operand("x", x, None, K)
+    _check_operand("w", w, None, K)
+    _check_operand("y", y, M, N // 2 if epilogue == EPILOGUE_SILU_MUL else N)
+    if not (x.device == w.device == y.device) or x.device.type != "cuda":
+        raise ValueError(f"operands must be on one GPU, got {x.device}, {w.device}, {y.device}")
+    with torch.cuda.device(x.device):
+        rc = _lib.load().krk_gemm_bf16_noalloc(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
+                                               y.stride(0), M, N, K, epilogue,
+                                               torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc)
     return y
 

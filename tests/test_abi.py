@@ -458,3 +458,13 @@ def test_package_loads_under_another_name():
     assert krk._lib.LIB_PATH == kernels._lib.LIB_PATH
     assert krk_loader.load("krk_alias_for_test") is krk
     assert krk.tune.candidates(1, 6144, 2560)[0] == kernels.gemm.plan(1, 6144, 2560)
+
+
+def test_noalloc_rejects_before_touching_the_device(lib):
+    """krk_gemm_bf16_noalloc checks the shape and whether the plan's split-K
+    partials fit the static scratch before any device call (fake pointers)."""
+    rc = lib.krk_gemm_bf16_noalloc(X, 2560, W, 2560, Y, 6144, 0, 6144, 2560, NONE, None)
+    assert rc == _lib.KRK_ERR_INVALID
+    # M=8, N=65536, K=32768: the plan splits K 8 ways, 16 MiB of partials
+    rc = lib.krk_gemm_bf16_noalloc(X, 32768, W, 32768, Y, 65536, 8, 65536, 32768, NONE, None)
+    assert rc == _lib.KRK_ERR_WORKSPACE and "static scratch" in _lib.last_error()
