@@ -118,6 +118,12 @@ typedef struct krk_gemm_config {
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
     int k_chunk;  /* MFMA_LDS: k per pipeline stage, 256 or 512 (512 needs
                      m_tiles + n_tiles <= 4); other kernels: ignored */
+    int prologue; /* normed calls (krk_gemm_bf16_normed_config): 0 = the plan's way
+                     (a separate prologue kernel, or inside the VALU kernel at
+                     M = 1); 1 = inside a STREAM kernel at any M, computed by
+                     producer waves and handed to the other workgroups through
+                     the workspace (K <= 4096, at most 5 K stages per split).
+                     Ignored by plain calls. */
 } krk_gemm_config;
 
 /*
@@ -198,9 +204,11 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx,
  *              leaves them zero); the rest is scratch.
  *
  * At M = 1, VALU plans of at most 2048 workgroups run the prologue inside the
- * projection kernel (one launch); krk_gemm_normed_fused tells which.  Other
- * calls run a one-workgroup-per-row prologue kernel that writes xout and the
- * normalised rows into the workspace, then the projection.
+ * projection kernel (one launch); so do STREAM configurations with
+ * prologue = 1 at any M (krk_gemm_normed_fused tells which).  Other calls run
+ * a one-workgroup-per-row prologue kernel that writes xout and the
+ * normalised rows into the workspace, then the projection: measured faster
+ * than the in-kernel hand-off at M >= 2, so the plan uses it there.
  */
 int krk_gemm_bf16_normed(const void* x, int64_t ldx, const void* d, int64_t ldd,
                          const void* w_norm, float eps, void* xout, int64_t ldxo,

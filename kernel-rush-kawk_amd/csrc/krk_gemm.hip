@@ -8,6 +8,7 @@
 // touches device memory from the host, so every call is graph-capturable.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
@@ -92,7 +93,7 @@ struct TableEntry {
     krk_gemm_config cfg;  // m_tiles 0: derived from M
 };
 constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits, int k_chunk = 0) {
-    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk};
+    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk, 0};
 }
 // VALU entries: n_tiles = W rows per wave, unroll = 512-k blocks in flight per
 // row (0: enough to cover a split's K range in one pass).  MFMA_LDS entries: unroll = stages in
@@ -308,6 +309,8 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
     auto_config(M, N, K, epilogue, &a);
     if (!in) { *out = a; return KRK_OK; }
     krk_gemm_config c = *in;
+    if (c.prologue != 0 && c.prologue != 1)
+        return fail(KRK_ERR_UNSUPPORTED, "prologue=%d not in {0, 1}", c.prologue);
     if (c.kernel == KRK_KERNEL_AUTO) c.kernel = a.kernel;
     const bool same_kernel = c.kernel == a.kernel;
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
@@ -551,9 +554,10 @@ int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int XS, bool SILU, int SK = 0>
-int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {}) {
-    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK>);
+template <int MT, int XS, bool SILU, int SK = 0, bool NORM = false>
+int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {},
+                  krk::CoopNorm cn = {}) {
+    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK, NORM>);
     size_t shm = krk::stream_lds_bytes(MT, depth);
     const int G = stream_groups(nblocks, a.splits);
     // Unsplit K: the rest of the LDS holds finished blocks until the end.
@@ -573,7 +577,7 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     const int groups = G * a.splits;
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
                     (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth, (void*)&obcap,
-                    (void*)&a.part, (void*)&a.ctr, (void*)&sa};
+                    (void*)&a.part, (void*)&a.ctr, (void*)&sa, (void*)&cn};
     hipError_t e = hipLaunchKernel(fn, dim3(groups), dim3(64 * krk::kStreamWaves), args, shm, stream);
     return hip_status(e, "stream_gemm_kernel launch");
 }
@@ -623,6 +627,31 @@ int dispatch_stream_sel(const LaunchArgs& a, const krk_gemm_config& c, int nbloc
         }
     }
     return fail(KRK_ERR_UNSUPPORTED, "STREAM selection epilogue: m_tiles=%d", c.m_tiles);
+}
+
+// Normed stream calls compute the RMSNorm prologue in the kernel
+// (krk_coop.h); instantiated for a split's K range of 4 or 5 stages (K up
+// to 2560, the hidden size every normed projection reads).
+template <int MT, bool SILU>
+int dispatch_stream_norm_xs(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                            const krk::CoopNorm& cn) {
+    switch (stream_xs(MT, cdiv(cdiv(a.K, krk::kStreamKC), c.splits))) {
+        case 4: return launch_stream<MT, 4, SILU, 0, true>(a, nblocks, c.unroll, s, {}, cn);
+        case 5: return launch_stream<MT, 5, SILU, 0, true>(a, nblocks, c.unroll, s, {}, cn);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "STREAM normed: no instantiation for m_tiles=%d and this K split", MT);
+}
+
+template <bool SILU>
+int dispatch_stream_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                         const krk::CoopNorm& cn) {
+    switch (c.m_tiles) {
+        case 1: return dispatch_stream_norm_xs<1, SILU>(a, c, nblocks, s, cn);
+        case 2: return dispatch_stream_norm_xs<2, SILU>(a, c, nblocks, s, cn);
+        case 3: return dispatch_stream_norm_xs<3, SILU>(a, c, nblocks, s, cn);
+        case 4: return dispatch_stream_norm_xs<4, SILU>(a, c, nblocks, s, cn);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
 
 template <bool SILU>
@@ -737,7 +766,41 @@ constexpr int kNormFusedMaxGroups = 2048;
 
 // Whether a resolved configuration runs the RMSNorm prologue inside the VALU
 // kernel (else a separate prologue kernel writes the normalised rows first).
+// Fault injection for tests of the in-kernel prologue's bounded wait:
+// KRK_COOP_PRODUCERS=0 turns the producer waves off (every workgroup then
+// times out and computes the rows itself) and KRK_COOP_WAIT_US sets the bound
+// of the wait (default 30 us).  Read at every call.
+int coop_producers_enabled() {
+    const char* e = getenv("KRK_COOP_PRODUCERS");
+    return (e && e[0] == '0' && e[1] == '\0') ? 0 : 1;
+}
+uint32_t coop_wait_ticks() {
+    const char* e = getenv("KRK_COOP_WAIT_US");
+    if (!e || !*e) return krk::kCoopWaitTicks;
+    const long us = strtol(e, nullptr, 10);
+    return us >= 1 && us <= 1000000 ? (uint32_t)(us * 100) : krk::kCoopWaitTicks;
+}
+
+// Whether a STREAM configuration can compute the prologue in the kernel
+// (krk_coop.h): instantiated for up to 5 K stages per split.
+bool coop_capable(int K, const krk_gemm_config& c) {
+    if (c.kernel != KRK_KERNEL_STREAM || K > krk::kCoopMaxK) return false;
+    const int xs = stream_xs(c.m_tiles, cdiv(cdiv(K, krk::kStreamKC), c.splits));
+    return xs == 4 || xs == 5;
+}
+
+// In-kernel prologue: asked for by the configuration (prologue = 1).  The
+// plan never asks: at gate_up M = 32 the hand-off took the stream kernel
+// from 23.5 to 33.5 us against 27.2 us for the prologue kernel + projection
+// (producer loads ~2 us, their stores ~2.5 us, the flag's trip through
+// device-coherent memory and the polls 1.5-3 us; measured per workgroup).
+bool norm_coop(int M, int K, const krk_gemm_config& c) {
+    (void)M;
+    return c.prologue == 1 && coop_capable(K, c);
+}
+
 bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
+    if (norm_coop(M, K, c)) return true;
     if (c.kernel != KRK_KERNEL_VALU || M != 1 || c.unroll != kValuNormDepth) return false;
     const Geometry g = geometry(M, N, epilogue, c);
     return (int64_t)g.nblocks * c.splits <= kNormFusedMaxGroups &&
@@ -757,16 +820,24 @@ struct NormSpec {
 // Workspace of a call: [split-K counters and partials][normalised rows
 // M x K bf16 when a separate prologue writes them].
 struct WorkspaceLayout {
-    size_t gemm;    // split-K part, at offset 0
-    size_t n_off;   // offset of the normalised rows (0 if none)
+    size_t gemm;         // split-K part, at offset 0
+    size_t n_off;        // offset of the normalised rows, or of the in-kernel prologue's control block (0 if none)
+    size_t coop_copies;  // offset of the in-kernel prologue's per-die copies (0 if none)
+    int64_t slot_elems;  // elements per copy
     size_t total;
 };
 WorkspaceLayout workspace_layout(int M, int N, int K, int epilogue, const krk_gemm_config& c, bool normed) {
     WorkspaceLayout l;
     l.gemm = workspace_for(M, N, epilogue, c);
     const bool prologue = normed && !norm_fused(M, N, K, epilogue, c);
-    l.n_off = prologue ? align_up(l.gemm, 256) : 0;
-    l.total = prologue ? l.n_off + (size_t)M * K * sizeof(uint16_t) : l.gemm;
+    const bool coop = normed && norm_coop(M, K, c);
+    l.n_off = (prologue || coop) ? align_up(l.gemm, 256) : 0;
+    l.coop_copies = coop ? l.n_off + align_up(krk::coop_ctl_bytes(), 256) : 0;
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    l.slot_elems = coop ? (int64_t)(krk::coop_slot_bytes(Mc, K, c.m_tiles) / sizeof(uint16_t)) : 0;
+    l.total = prologue ? l.n_off + (size_t)M * K * sizeof(uint16_t)
+              : coop   ? l.coop_copies + krk::coop_copy_bytes(Mc, K, c.m_tiles)
+                       : l.gemm;
     return l;
 }
 
@@ -849,6 +920,7 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     if (ns) na = krk::NormArgs{static_cast<const uint16_t*>(ns->d), ns->ldd, static_cast<const uint16_t*>(ns->w_norm),
                                ns->eps, static_cast<uint16_t*>(ns->xout), ns->ldxo};
     const bool fused = ns && norm_fused(M, N, K, epilogue, c);
+    const bool coop = ns && norm_coop(M, K, c);
     // Projection input: x itself, or the normalised rows a prologue kernel
     // writes into the workspace.
     const uint16_t* xin = static_cast<const uint16_t*>(x);
@@ -877,7 +949,24 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
         a.splits = c.splits;
         a.part = part;
         a.ctr = ctr;
-        if (fused) {
+        if (fused && coop) {
+            // This chunk's rows of x, d and xout; the control block and the
+            // copies are reused by the chunks in stream order.
+            krk::CoopNorm cn;
+            cn.x = static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx;
+            cn.ldx = ldx;
+            cn.na = na;
+            cn.na.d += (int64_t)m0 * na.ldd;
+            cn.na.xout += (int64_t)m0 * na.ldxo;
+            cn.ctl = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + wl.n_off);
+            cn.copies = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + wl.coop_copies);
+            cn.slot_elems = wl.slot_elems;
+            cn.M = a.M;
+            cn.K = K;
+            cn.producers = coop_producers_enabled();
+            cn.wait_ticks = coop_wait_ticks();
+            rc = silu ? dispatch_stream_norm<true>(a, c, g.nblocks, st, cn) : dispatch_stream_norm<false>(a, c, g.nblocks, st, cn);
+        } else if (fused) {
             rc = silu ? dispatch_valu_norm<true>(a, c, g.nblocks, st, na) : dispatch_valu_norm<false>(a, c, g.nblocks, st, na);
         } else if (c.kernel == KRK_KERNEL_MFMA) {
             rc = silu ? dispatch_mfma<true>(a, c, g.nblocks, st) : dispatch_mfma<false>(a, c, g.nblocks, st);

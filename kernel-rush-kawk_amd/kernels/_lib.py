@@ -41,7 +41,7 @@ _size = ctypes.c_size_t
 
 
 class GemmConfig(ctypes.Structure):
-    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk."""
+    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk, prologue."""
 
     _fields_ = [
         ("kernel", _int),
@@ -51,6 +51,7 @@ class GemmConfig(ctypes.Structure):
         ("waves", _int),
         ("splits", _int),
         ("k_chunk", _int),
+        ("prologue", _int),
     ]
 
     def as_dict(self) -> dict:

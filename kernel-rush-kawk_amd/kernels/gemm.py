@@ -490,8 +490,16 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
                 if not ok:
                     return ok, why
             return ok, why
+    extra = []
+    if norm is not None:
+        # Stream configurations can also compute the prologue in the kernel
+        # (prologue = 1); timed as whole normed calls like every candidate.
+        for cfg in tune.candidates(M, N, K, epilogue):
+            if cfg["kernel"] == _lib.KERNEL_STREAM and normed_fused(M, N, K, epilogue, dict(cfg, prologue=1)):
+                extra.append(dict(cfg, prologue=1))
     timer = lambda fn, rot_: _time(fn, rotate=rot_)
-    return tune.search(kind, M, N, K, epilogue, a.device, build, accept, timer, rot, log=log, cache=cache, limit=limit)
+    return tune.search(kind, M, N, K, epilogue, a.device, build, accept, timer, rot, log=log, cache=cache, limit=limit,
+                       extra=extra)
 
 
 def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = None, tune: bool = True, cache=None):

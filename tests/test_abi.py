@@ -265,22 +265,44 @@ def test_normed_argument_errors(lib, kw, code, msg):
     assert msg in _lib.last_error()
 
 
-def test_normed_fused_only_at_m1_with_a_modest_grid(lib):
-    """M = 1 VALU plans of up to 2048 workgroups fuse the prologue (qkv,
-    gate_up); lm_head's 19k-workgroup plan and every M > 1 run the separate
-    prologue kernel."""
+def test_normed_fused_plans(lib):
+    """The plans fuse the prologue at M = 1 on VALU plans of up to 2048
+    workgroups (qkv, gate_up); elsewhere they run the separate prologue
+    kernel first.  A stream configuration with prologue = 1 computes it in
+    the kernel at any M."""
     for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["gate_up"], 1, 1), (QWEN["qkv"], 4, 0),
                                   (QWEN["gate_up"], 8, 0), (QWEN["lm_head"], 1, 0), (QWEN["qkv"], 32, 0),
                                   (QWEN["gate_up"], 32, 0), (QWEN["lm_head"], 64, 0)]:
         assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == fused, (N, M)
+    coop = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1)
+    for (N, K, epi), M in [(QWEN["gate_up"], 9), (QWEN["gate_up"], 32), (QWEN["gate_up"], 64),
+                           (QWEN["lm_head"], 5), (QWEN["lm_head"], 64), (QWEN["qkv"], 2)]:
+        assert lib.krk_gemm_normed_fused(M, N, K, epi, ctypes.byref(coop)) == 1, (N, M)
+    deep = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1, splits=1)
+    assert lib.krk_gemm_normed_fused(8, 2560, 9728, NONE, ctypes.byref(deep)) < 0  # 19 stages: not instantiated
+    bad = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=2)
+    assert lib.krk_gemm_normed_fused(8, 6144, 2560, NONE, ctypes.byref(bad)) == _lib.KRK_ERR_UNSUPPORTED
     assert lib.krk_gemm_normed_fused(0, 6144, 2560, NONE, None) == _lib.KRK_ERR_INVALID
 
 
-def test_normed_workspace_adds_the_normalised_rows(lib):
-    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["gate_up"], 64), (QWEN["lm_head"], 17), (QWEN["qkv"], 100)]:
+COOP_CTL_BYTES = 4 * (16 * 64 + 64 + 32 + 32)  # control block of the in-kernel prologue
+
+
+def test_normed_workspace_layouts(lib):
+    """Prologue-kernel plans add the M normalised rows after the split-K area;
+    in-kernel-prologue (stream) plans add the control block and one copy of
+    the rows per die slot (16); fused VALU plans at M = 1 add nothing."""
+    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["qkv"], 4), (QWEN["qkv"], 100), (QWEN["gate_up"], 64),
+                           (QWEN["lm_head"], 17)]:
         plain = lib.krk_gemm_workspace_bytes(M, N, K, epi)
         normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None)
         assert normed == -(-plain // 256) * 256 + M * K * 2
+    coop = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1)
+    for (N, K, epi), M in [(QWEN["gate_up"], 64), (QWEN["lm_head"], 17), (QWEN["gate_up"], 100)]:
+        plain = lib.krk_gemm_config_workspace_bytes(M, N, K, epi, ctypes.byref(coop))
+        normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, ctypes.byref(coop))
+        tiles = -(-min(M, 64) // 16)  # the stream plan's 16-row tiles; the copies are in its fragment layout
+        assert normed == -(-plain // 256) * 256 + -(-COOP_CTL_BYTES // 256) * 256 + 16 * tiles * 16 * K * 2, (N, M)
     for (N, K, epi), M in [(QWEN["qkv"], 1), (QWEN["gate_up"], 1)]:
         assert lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None) == lib.krk_gemm_workspace_bytes(M, N, K, epi)
 

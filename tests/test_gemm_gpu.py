@@ -727,19 +727,34 @@ EPS = 1e-6
 QWEN = {"qkv": (2560, 6144, NONE), "gate_up": (2560, 19456, SILU), "lm_head": (2560, 151936, NONE)}
 
 
-def krk_normed(x, y, wn, w, epilogue=NONE, config=None, device="cuda:0"):
-    """Normed HIP call on CPU bf16 inputs; returns (xout, out) on the CPU."""
+def krk_normed(x, y, wn, w, epilogue=NONE, config=None, device="cuda:0", ws=None, with_ws=False):
+    """Normed HIP call on CPU bf16 inputs; returns (xout, out) on the CPU
+    (and the workspace with ``with_ws``).  Outputs start NaN-filled."""
     M, K = x.shape
     N = w.shape[0]
     nout = N // 2 if epilogue == SILU else N
     xd, yd, gd, wd = x.to(device), y.to(device), wn.to(device), w.to(device)
-    out = torch.empty((M, nout), dtype=torch.bfloat16, device=device)
-    xout = torch.empty((M, K), dtype=torch.bfloat16, device=device)
-    nbytes = G.workspace_bytes(M, N, K, epilogue, config, normed=True)
-    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+    out = torch.full((M, nout), float("nan"), dtype=torch.bfloat16, device=device)
+    xout = torch.full((M, K), float("nan"), dtype=torch.bfloat16, device=device)
+    if ws is None:
+        nbytes = G.workspace_bytes(M, N, K, epilogue, config, normed=True)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes else None
     G.gemm_into(xd, wd, out, epilogue, ws, config, norm=(yd, gd, xout, EPS))
     torch.cuda.synchronize()
+    if with_ws:
+        return xout.cpu(), out.cpu(), ws
     return xout.cpu(), out.cpu()
+
+
+# The in-kernel prologue's control block (u32 words) sits after the split-K
+# area, padded to 256 bytes: [16 dies x 64 rows flags][64 claims][pad 32]
+# [fallbacks (cumulative)] -- the layout of csrc/krk_coop.h.
+COOP_FLAGS, COOP_CLAIMS, COOP_FALLBACKS = 0, 16 * 64, 16 * 64 + 64 + 32
+
+
+def coop_ctl(ws, M, N, K, epi, config=None):
+    off = -(-G.workspace_bytes(M, N, K, epi, config) // 256) * 256
+    return ws[off:off + 4 * (COOP_FALLBACKS + 1)].view(torch.int32).cpu()
 
 
 def _norm_inputs(M, K, seed):
@@ -790,6 +805,66 @@ def test_normed_fused_and_prologue_paths_agree(device, M, N, K, epi):
     assert ran >= 3
 
 
+@pytest.mark.parametrize("shape,M", [("gate_up", M) for M in (9, 16, 32, 64)] +
+                                    [("lm_head", M) for M in (5, 32, 64)])
+def test_normed_in_kernel_prologue(device, shape, M):
+    """Stream configurations with prologue = 1 compute rms_norm(x + y) inside
+    the projection kernel (one launch): parity with the oracle, xout bit-exact, every row produced by
+    the producer waves (no workgroup had to fall back), the control block
+    back at zero after the call, and a second call with other inputs on the
+    same workspace correct too."""
+    K, N, epi = QWEN[shape]
+    cfg = dict(G.plan(M, N, K, epi), prologue=1)
+    assert G.normed_fused(M, N, K, epi, cfg), "stream plans can run the prologue in the kernel"
+    w = R.randn_bf16((N, K), 9320 + M, 0.02)
+    ws = None
+    for rep in range(2):
+        x, y, wn = _norm_inputs(M, K, 9330 + 10 * rep + M)
+        say("normed in-kernel prologue", shape, M, rep)
+        xo, out, ws = krk_normed(x, y, wn, w, epi, cfg, ws=ws, with_ws=True)
+        _check_normed(x, y, wn, w, epi, xo, out, f"normed in-kernel {shape} M={M} call {rep}")
+        ctl = coop_ctl(ws, M, N, K, epi, cfg)
+        assert int(ctl[COOP_FALLBACKS]) == 0, "a workgroup timed out waiting for the producer waves"
+        assert int(ctl[:COOP_FALLBACKS].abs().sum()) == 0, "control block not cleared after the call"
+
+
+@pytest.mark.parametrize("M,N,K,epi,splits", [(3, 1040, 2560, NONE, 1), (17, 600, 2048, SILU, 2), (40, 2064, 1000, NONE, 1),
+                                              (64, 496, 2560, SILU, 5), (8, 4100, 2560, NONE, 3)])
+def test_normed_in_kernel_prologue_configs(device, M, N, K, epi, splits):
+    """The in-kernel prologue under stream configurations of every row-tile
+    count, split K and ragged K and N, against the oracle; deterministic."""
+    x, y, wn = _norm_inputs(M, K, 9800 + M)
+    w = R.randn_bf16((N, K), 9810 + M, 0.02)
+    cfg = dict(kernel=_lib.KERNEL_STREAM, splits=splits, prologue=1)
+    assert G.normed_fused(M, N, K, epi, cfg)
+    say("normed in-kernel config", M, N, K, epi, cfg)
+    xo, out, ws = krk_normed(x, y, wn, w, epi, cfg, with_ws=True)
+    _check_normed(x, y, wn, w, epi, xo, out, f"normed in-kernel {cfg}")
+    assert torch.equal(out, krk_normed(x, y, wn, w, epi, cfg, ws=ws)[1])
+    assert int(coop_ctl(ws, M, N, K, epi, cfg)[COOP_FALLBACKS]) == 0
+
+
+def test_normed_in_kernel_prologue_fallback(device, monkeypatch):
+    """With the producer waves switched off from the host, every workgroup's
+    bounded wait runs out and it computes the rows itself: the result is
+    still the oracle's, and every workgroup counted a fallback."""
+    M, N, K, epi = 16, 19456, 2560, SILU
+    monkeypatch.setenv("KRK_COOP_PRODUCERS", "0")
+    monkeypatch.setenv("KRK_COOP_WAIT_US", "2")
+    x, y, wn = _norm_inputs(M, K, 9850)
+    w = R.randn_bf16((N, K), 9851, 0.02)
+    cfg = dict(G.plan(M, N, K, epi), prologue=1)
+    say("normed in-kernel fallback", M, N, K)
+    xo, out, ws = krk_normed(x, y, wn, w, epi, cfg, with_ws=True)
+    _check_normed(x, y, wn, w, epi, xo, out, "normed in-kernel, producers off")
+    ctl = coop_ctl(ws, M, N, K, epi, cfg)
+    assert int(ctl[COOP_FALLBACKS]) >= 1
+    assert int(ctl[:COOP_FALLBACKS].abs().sum()) == 0
+    monkeypatch.delenv("KRK_COOP_PRODUCERS")
+    xo2, out2 = krk_normed(x, y, wn, w, epi, cfg, ws=ws)
+    assert torch.equal(out2, out) and torch.equal(xo2, xo)
+
+
 def test_normed_rows_beyond_64(device):
     M, N, K = 100, 384, 2560
     x, y, wn = _norm_inputs(M, K, 9500)
@@ -817,10 +892,13 @@ def test_add_rms_norm_kernel(device, M, K):
 def test_normed_graph_replay(device):
     """Fused and prologue-kernel normed calls captured in one graph replay to
     the eager results, with eager work between replays."""
-    cases = [(1, 6144, 2560, NONE), (8, 19456, 2560, SILU), (32, 6144, 2560, NONE)]
+    cases = [(1, 6144, 2560, NONE, None), (8, 19456, 2560, SILU, None), (32, 6144, 2560, NONE, None),
+             (32, 19456, 2560, SILU, None), (32, 19456, 2560, SILU, {"kernel": _lib.KERNEL_STREAM, "prologue": 1}),
+             (64, 151936, 2560, NONE, {"kernel": _lib.KERNEL_STREAM, "prologue": 1})]
     ops, ins, eager, outs = [], [], [], []
-    for i, (M, N, K, epi) in enumerate(cases):
-        op = G.SkinnyGateUp(M, N // 2, K, device) if epi == SILU else G.SkinnyMatmul(M, N, K, device)
+    for i, (M, N, K, epi, cfg) in enumerate(cases):
+        op = (G.SkinnyGateUp(M, N // 2, K, device, config=cfg) if epi == SILU
+              else G.SkinnyMatmul(M, N, K, device, config=cfg))
         x, y, wn = (t.to(device) for t in _norm_inputs(M, K, 9700 + i))
         w = R.randn_bf16((N, K), 9710 + i, 0.02).to(device)
         xo = torch.empty_like(x)
