@@ -116,13 +116,12 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 16, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
     {2560, 9728, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 2, 8, 3)},
     {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 9728, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 9728, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // lm_head 2560 -> 151936
@@ -130,8 +129,7 @@ const TableEntry kTable[] = {
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 5, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 33, 48, kcfg(KRK_KERNEL_STREAM, 1, 3, 0, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
 
     // One GPU's shard under 8-way tensor parallelism (QKV, gate_up and
     // lm_head split along N, o and down along K), from the warm-up tuner's
@@ -281,11 +279,14 @@ int stream_xs(int MT, int nst) {
     return 0;
 }
 // Deepest ring that leaves room for one output-buffer block.
-inline int stream_max_depth(int MT) {
+inline int stream_max_depth(int MT, int nred) {
     int d = krk::kStreamMaxDepth;
-    while (d > 2 && krk::stream_lds_bytes(MT, d) + krk::stream_out_bytes(MT, false) > kLdsMax) --d;
+    while (d > 2 && krk::stream_lds_bytes(MT, d, nred) + krk::stream_out_bytes(MT, false) > kLdsMax) --d;
     return d;
 }
+// Reduction areas of a stream launch: one when every split owns two or more
+// K stages.
+inline int stream_nred_for(int K, int splits) { return krk::stream_nred(cdiv(K, krk::kStreamKC) / splits); }
 // Persistent grid: workgroups per split, at most one per CU, chosen so the
 // blocks divide as evenly as possible (a 1.25x overload costs more than
 // leaving CUs idle).
@@ -374,7 +375,7 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
         if (stream_xs(c.m_tiles, cdiv(cdiv(K, krk::kStreamKC), c.splits)) == 0)
             return fail(KRK_ERR_UNSUPPORTED, "STREAM keeps x in registers: %d K stages per split x %d m tiles is too "
                         "many (raise splits)", cdiv(cdiv(K, krk::kStreamKC), c.splits), c.m_tiles);
-        const int maxd = stream_max_depth(c.m_tiles);
+        const int maxd = stream_max_depth(c.m_tiles, stream_nred_for(K, c.splits));
         if (!c.unroll) c.unroll = same_kernel && a.unroll ? a.unroll : maxd;
         if (c.unroll < 2 || c.unroll > maxd)
             return fail(KRK_ERR_UNSUPPORTED, "STREAM depth (unroll) %d not in 2..%d", c.unroll, maxd);
@@ -558,7 +559,8 @@ template <int MT, int XS, bool SILU, int SK = 0, bool NORM = false>
 int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {},
                   krk::CoopNorm cn = {}) {
     const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK, NORM>);
-    size_t shm = krk::stream_lds_bytes(MT, depth);
+    int nred = stream_nred_for(a.K, a.splits);
+    size_t shm = krk::stream_lds_bytes(MT, depth, nred);
     const int G = stream_groups(nblocks, a.splits);
     // Unsplit K: the rest of the LDS holds finished blocks until the end.
     int obcap = 0;
@@ -577,7 +579,7 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     const int groups = G * a.splits;
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
                     (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth, (void*)&obcap,
-                    (void*)&a.part, (void*)&a.ctr, (void*)&sa, (void*)&cn};
+                    (void*)&nred, (void*)&a.part, (void*)&a.ctr, (void*)&sa, (void*)&cn};
     hipError_t e = hipLaunchKernel(fn, dim3(groups), dim3(64 * krk::kStreamWaves), args, shm, stream);
     return hip_status(e, "stream_gemm_kernel launch");
 }
@@ -1461,7 +1463,7 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
         for (int pf : {2, 3})
             for (int kc : {256, 512})
                 for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc});
-    for (int d = 2; d <= 5; ++d)
+    for (int d = 2; d <= krk::kStreamMaxDepth; ++d)
         for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});
     for (int nt : nts)
         for (int sp : {1, 2, 4}) add(krk_gemm_config{KRK_KERNEL_MFMA, 0, nt, 4, 4, sp, 0});

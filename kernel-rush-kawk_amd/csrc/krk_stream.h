@@ -47,11 +47,17 @@ constexpr int kStreamKPW = (kStreamKC / 32) / kStreamWaves;  // k-steps per wave
 constexpr int kStreamLPW = 16 / kStreamWaves;                // DMAs per wave per stage (2)
 constexpr int kStreamMaxDepth = 8;
 
-// Bytes of dynamic LDS: two reduction areas [WV][MT][64] f32x4 (blocks
-// alternate between them), then the ring.
+// Bytes of dynamic LDS: `nred` reduction areas [WV][MT][64] f32x4, then the
+// ring.  A block's partial sums are parked at its end and reduced during the
+// next block's first stage.  With two or more stages per block one area
+// suffices (the next block parks its sums only after its second stage's
+// barrier, which every wave reaches after that reduction); with one stage
+// per block the blocks alternate between two.  The area saved goes to the
+// ring (measured: at 64 rows two areas left room for only 4 stages).
 __host__ __device__ constexpr size_t stream_red_bytes(int MT) { return (size_t)kStreamWaves * MT * 64 * 16; }
-__host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth) {
-    return 2 * stream_red_bytes(MT) + (size_t)depth * kStreamSlot;
+__host__ __device__ constexpr int stream_nred(int stages_per_split) { return stages_per_split >= 2 ? 1 : 2; }
+__host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth, int nred) {
+    return (size_t)nred * stream_red_bytes(MT) + (size_t)depth * kStreamSlot;
 }
 // Output buffer behind the ring (unsplit K): the bf16 results of `obcap`
 // blocks, [slot][16·MT rows][CB channels].
@@ -89,7 +95,7 @@ __global__ void __launch_bounds__(512)
 stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                    const uint16_t* __restrict__ w, int64_t ldw,
                    uint16_t* __restrict__ y, int64_t ldy,
-                   int M, int N, int K, int splits, int depth, int obcap,
+                   int M, int N, int K, int splits, int depth, int obcap, int nred,
                    float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa, CoopNorm cn) {
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     constexpr bool SEL = SK > 0;
@@ -103,8 +109,8 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     f32x4* const red0 = reinterpret_cast<f32x4*>(smem);
-    f32x4* const red1 = red0 + WV * MT * 64;
-    unsigned char* const ring = smem + 2 * stream_red_bytes(MT);
+    f32x4* const red1 = nred == 2 ? red0 + WV * MT * 64 : red0;
+    unsigned char* const ring = smem + nred * stream_red_bytes(MT);
     uint16_t* const ob = reinterpret_cast<uint16_t*>(ring + (size_t)depth * kStreamSlot);
     constexpr int MP = 16 * MT;  // rows per output-buffer slot
 
@@ -202,10 +208,10 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 XR[j][i] = (kok && m < M) ? v : u32x4{0u, 0u, 0u, 0u};
             }
         }
-        // Each stage's rows go through LDS (the reduction areas, 16·MT rows of
-        // 1 KB, idle until the first block ends; chunks XOR-swizzled by row so the
-        // fragment reads hit distinct banks) and come back as this wave's MFMA
-        // fragments X[j][kk][i].
+        // Each stage's rows go through LDS (16·MT rows of 1 KB at the start of
+        // the area, idle until the ring starts and the first block ends;
+        // chunks XOR-swizzled by row so the fragment reads hit distinct
+        // banks) and come back as this wave's MFMA fragments X[j][kk][i].
         unsigned char* const xstage = smem;
 #pragma unroll
         for (int j = 0; j < XS; ++j) {
