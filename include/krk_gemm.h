@@ -124,6 +124,12 @@ typedef struct krk_gemm_config {
                      producer waves and handed to the other workgroups through
                      the workspace (K <= 4096, at most 5 K stages per split).
                      Ignored by plain calls. */
+    int channels; /* MFMA_LDS: output channels per workgroup, a multiple of 8 up
+                     to 16·n_tiles (8·n_tiles with SILU_MUL); 0 = all of them.
+                     Fewer channels than the tiles hold leave the rest of the
+                     last tile as padding (not loaded), so a shape can be cut
+                     into exactly as many blocks as there are CUs.  Other
+                     kernels: ignored. */
 } krk_gemm_config;
 
 /*

@@ -74,6 +74,8 @@ Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
         g.cb = c.waves * (silu ? c.n_tiles / 2 : c.n_tiles);  // n_tiles W rows per wave
     } else if (c.kernel == KRK_KERNEL_STREAM) {
         g.cb = silu ? 8 : 16;  // one 16-row tile: 16 channels, or 8 gate + 8 up rows
+    } else if (c.kernel == KRK_KERNEL_MFMA_LDS && c.channels > 0) {
+        g.cb = c.channels;
     } else {
         g.cb = 16 * (silu ? c.n_tiles / 2 : c.n_tiles);
     }
@@ -92,25 +94,27 @@ struct TableEntry {
     int N, K, epilogue, m_lo, m_hi;
     krk_gemm_config cfg;  // m_tiles 0: derived from M
 };
-constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits, int k_chunk = 0) {
-    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk, 0};
+constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits, int k_chunk = 0,
+                               int channels = 0) {
+    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk, 0, channels};
 }
 // VALU entries: n_tiles = W rows per wave, unroll = 512-k blocks in flight per
 // row (0: enough to cover a split's K range in one pass).  MFMA_LDS entries: unroll = stages in
-// flight, k_chunk 0 = 512 where it fits.
+// flight, k_chunk 0 = 512 where it fits, channels 0 = all of the tiles' channels.
 const TableEntry kTable[] = {
     // qkv 2560 -> 6144
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 5, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 2, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
+    // 256 blocks of 24 channels: one per CU, whole K
+    {6144, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1, 512, 24)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256, 24)},
     // o_proj 4096 -> 2560
     {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 3, 8, kcfg(KRK_KERNEL_VALU, 2, 4, 8, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 25, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
@@ -121,9 +125,9 @@ const TableEntry kTable[] = {
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
     {2560, 9728, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 2, 8, 3)},
     {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 512)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 17, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     // lm_head 2560 -> 151936
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
@@ -212,6 +216,7 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
                 c->waves = krk::kLdsWaves;
                 c->unroll = c->unroll ? c->unroll : 2;
                 c->k_chunk = c->k_chunk ? c->k_chunk : default_kc(mt, c->n_tiles);
+                c->channels = c->channels ? c->channels : 16 * (silu ? c->n_tiles / 2 : c->n_tiles);
             }
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
             if (c->kernel == KRK_KERNEL_VALU) {
@@ -253,7 +258,8 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
         r.unroll = 2;
         r.k_chunk = default_kc(mt, r.n_tiles);
         r.waves = krk::kLdsWaves;
-        const int nblocks = cdiv(Nout, 16 * (silu ? r.n_tiles / 2 : r.n_tiles));
+        r.channels = 16 * (silu ? r.n_tiles / 2 : r.n_tiles);
+        const int nblocks = cdiv(Nout, r.channels);
         r.splits = 1;
         while (nblocks * r.splits < 192 && r.splits < 4 && KST >= 2 * (r.splits + 1)) ++r.splits;
     }
@@ -356,6 +362,11 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
                         "(2, or 3 when m_tiles + n_tiles <= %d)", c.unroll, c.m_tiles, c.n_tiles, kLdsPf3MaxTiles);
         if (c.splits < 1 || c.splits > 32)
             return fail(KRK_ERR_UNSUPPORTED, "splits=%d not in 1..32", c.splits);
+        const int full = 16 * (epilogue == KRK_EPILOGUE_SILU_MUL ? c.n_tiles / 2 : c.n_tiles);
+        if (!c.channels) c.channels = same_kernel && a.n_tiles == c.n_tiles && a.channels ? a.channels : full;
+        if (c.channels < 8 || c.channels > full || c.channels % 8)
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS channels=%d: a multiple of 8 in 8..%d for %d tiles", c.channels,
+                        full, c.n_tiles);
         *out = c;
         return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_STREAM) {
@@ -437,6 +448,7 @@ struct LaunchArgs {
     uint16_t* y;
     int64_t ldy;
     int M, N, K, splits;
+    int cb;  // output channels per block (MFMA_LDS)
     float* part;
     uint32_t* ctr;
 };
@@ -514,9 +526,10 @@ int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::S
         static std::atomic<uint64_t> done{0};
         const hipError_t attr = shm > 65536 ? ensure_lds_limit(fn, (int)shm, done) : hipSuccess;
         if (attr != hipSuccess) return hip_status(attr, "mfma_lds_kernel LDS attribute");
+        int cb = a.cb;
         void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
-                        (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&a.part, (void*)&a.ctr,
-                        (void*)&sa};
+                        (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&cb, (void*)&a.part,
+                        (void*)&a.ctr, (void*)&sa};
         hipError_t e = hipLaunchKernel(fn, dim3(nblocks * a.splits), dim3(64 * krk::kLdsWaves), args, shm, stream);
         return hip_status(e, "mfma_lds_kernel launch");
     }
@@ -951,6 +964,7 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
         a.splits = c.splits;
         a.part = part;
         a.ctr = ctr;
+        a.cb = g.cb;
         if (fused && coop) {
             // This chunk's rows of x, d and xout; the control block and the
             // copies are reused by the chunks in stream order.
@@ -1149,6 +1163,7 @@ int select_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
         a.K = K;
         a.splits = p.c.splits;
         a.ctr = p.c.splits > 1 ? reinterpret_cast<uint32_t*>(ws + l.proj) : nullptr;
+        a.cb = g.cb;
         a.part = p.c.splits > 1 ? reinterpret_cast<float*>(ws + l.proj + align_up((size_t)g.nblocks * sizeof(uint32_t), 256))
                                 : nullptr;
         krk::RowSelectArgs ra;
@@ -1434,7 +1449,7 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
     if (rc) return rc;
     if (cap < 0 || (cap > 0 && !out)) return fail(KRK_ERR_INVALID, "need an output array for cap=%d configurations", cap);
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
-    constexpr int kMax = 256;
+    constexpr int kMax = 1024;
     krk_gemm_config found[kMax];
     int n = 0;
     auto add = [&](const krk_gemm_config& want) {
@@ -1459,10 +1474,18 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
     // More splits for the weight-streaming MFMA kernels: at M >= 16 they cut
     // each workgroup's share of x, the bound of narrow-N, long-K shapes.
     const int wide_splits[] = {1, 2, 3, 4, 6, 8};
-    for (int nt : nts)
+    // LDS-staged: every tile width, each with all its channels and with
+    // fewer (the rest of the last tile padding), so a grid can match the CUs
+    // (qkv: 256 blocks of 24 channels).
+    for (int nt : nts) {
+        const int full = 16 * (epilogue == KRK_EPILOGUE_SILU_MUL ? nt / 2 : nt);
+        const int chans[] = {full, full - 8, full * 5 / 8 / 8 * 8, full / 2};
         for (int pf : {2, 3})
             for (int kc : {256, 512})
-                for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc});
+                for (int sp : wide_splits)
+                    for (int ch : chans)
+                        if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc, 0, ch});
+    }
     for (int d = 2; d <= krk::kStreamMaxDepth; ++d)
         for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});
     for (int nt : nts)

@@ -58,12 +58,17 @@ __host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool
 
 // SEL: per-workgroup argmax keys for token selection (krk_select.h) instead
 // of, or besides, storing y (y may be null); K unsplit.
+// cb: output channels per block (a multiple of 8, at most 16·NH).  Below
+// 16·NH the last tile is partly padding: its rows past cb are not loaded
+// (zeros in the tile) and their outputs not stored.  This lets a shape use
+// all 256 CUs with whole K (qkv: 6144 = 256 x 24 channels) instead of
+// leaving CUs idle or splitting K.
 template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false>
 __global__ void __launch_bounds__(64 * kLdsWaves)
 mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const uint16_t* __restrict__ w, int64_t ldw,
                 uint16_t* __restrict__ y, int64_t ldy,
-                int M, int N, int K, int splits,
+                int M, int N, int K, int splits, int cb,
                 float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa) {
     static_assert(!(SEL && SILU), "selection reads plain logits");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
@@ -91,16 +96,19 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int blk = blockIdx.x / splits;
     const int s = blockIdx.x - blk * splits;
     const int Nout = SILU ? (N >> 1) : N;
-    const int c0 = blk * (16 * NH);
+    const int c0 = blk * cb;
 
     // Row pieces this wave loads: tile rows RPL·(wave + WV·j) + lrow, W rows
     // first, then x rows.
     const uint16_t* rowp[LPW];
+    bool rowok[LW];  // the piece is one of the block's cb channels (else padding: zeros, not loaded)
 #pragma unroll
     for (int j = 0; j < LW; ++j) {
         const int tr = RPL * (wave + WV * j) + lrow;
         const int t = tr >> 4;
-        int ch = c0 + 16 * (t % NH) + (tr & 15);
+        const int cl = 16 * (t % NH) + (tr & 15);  // channel within the block
+        rowok[j] = cl < cb;
+        int ch = c0 + cl;
         ch = ch < Nout ? ch : Nout - 1;
         const int row = (SILU && t >= NH) ? ch + Nout : ch;
         rowp[j] = w + (int64_t)row * ldw + 8 * lsub;
@@ -129,7 +137,8 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         const int kk = st * KC + 8 * lsub < K ? st * KC : -8 * lsub;  // past K: the row's start
         const int xo = 8 * lsub < K ? 8 * lsub : K - 8;
 #pragma unroll
-        for (int j = 0; j < LW; ++j) R[j] = load_stream16(live ? rowp[j] + kk : x + xo);
+        for (int j = 0; j < LW; ++j)
+            R[j] = rowok[j] ? load_stream16(live ? rowp[j] + kk : x + xo) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < LX; ++j) R[LW + j] = load_cached16(live ? rowp[LW + j] + kk : x + xo);
     };
@@ -215,17 +224,19 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             gsum += red[((wv * MT + i) * NT + tl) * 64 + ln];
             if (SILU) usum += red[((wv * MT + i) * NT + tl + NH) * 64 + ln];
         }
-        const int c = c0 + 16 * tl + (ln & 15);
+        const int cl = 16 * tl + (ln & 15);
+        const int c = c0 + cl;
+        const bool cok = cl < cb && c < Nout;
         const int mb = 16 * i + 4 * (ln >> 4);
         if constexpr (SEL) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) selv[(mb + e) * (16 * NT) + 16 * tl + (ln & 15)] = (uint16_t)f32_to_bf16(gsum[e]);
-            if (y && c < Nout) {
+            if (y && cok) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (mb + e < M) o.put(mb + e, c, gsum[e], usum[e]);
             }
-        } else if (c < Nout) {
+        } else if (cok) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (mb + e < M) o.put(mb + e, c, gsum[e], usum[e]);
@@ -233,10 +244,10 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     }
     if constexpr (SEL) {
         __syncthreads();
-        const int n = 16 * NT < Nout - c0 ? 16 * NT : Nout - c0;
+        const int n = cb < Nout - c0 ? cb : Nout - c0;
         select_local(sa, selv, 16 * NT, n, c0, M, blockIdx.x);
     } else if (splits > 1) {
-        splitk_finish<SILU>(o, ctr, blk, c0, 16 * NH);
+        splitk_finish<SILU>(o, ctr, blk, c0, cb);
     }
 }
 

@@ -41,7 +41,7 @@ _size = ctypes.c_size_t
 
 
 class GemmConfig(ctypes.Structure):
-    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk, prologue."""
+    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk, prologue, channels."""
 
     _fields_ = [
         ("kernel", _int),
@@ -52,6 +52,7 @@ class GemmConfig(ctypes.Structure):
         ("splits", _int),
         ("k_chunk", _int),
         ("prologue", _int),
+        ("channels", _int),
     ]
 
     def as_dict(self) -> dict:

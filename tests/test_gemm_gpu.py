@@ -284,6 +284,7 @@ SPECIAL_FAMILIES = [
     ("valu x in registers", 2, dict(kernel=_lib.KERNEL_VALU, splits=2)),
     ("lds-staged", 16, dict(kernel=_lib.KERNEL_MFMA_LDS, splits=1)),
     ("lds-staged split-K", 24, dict(kernel=_lib.KERNEL_MFMA_LDS, splits=3)),
+    ("lds-staged 24 channels split-K", 20, dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=4, channels=24, splits=2)),
     ("stream", 33, dict(kernel=_lib.KERNEL_STREAM, splits=1)),
     ("stream split-K", 8, dict(kernel=_lib.KERNEL_STREAM, splits=2)),
     ("register mfma split-K", 13, dict(kernel=_lib.KERNEL_MFMA, splits=2)),
@@ -455,6 +456,30 @@ def test_all_lds_configs_agree(device, M, N, K):
     x = R.randn_bf16((M, K), 8700 + M)
     w = R.randn_bf16((N, K), 8701 + N, 0.02)
     _run_configs(x, w, NONE, _lds_configs(M, False))
+
+
+def _lds_channel_configs(M, silu):
+    """LDS-staged configurations whose blocks hold fewer channels than their
+    tiles: every multiple of 8 below the tiles' width."""
+    mt_min = -(-min(M, 64) // 16)
+    for mt, nt, sp in itertools.product(range(mt_min, 5), (1, 2, 4), (1, 3)):
+        if silu and nt % 2:
+            continue
+        full = 16 * (nt // 2 if silu else nt)
+        for ch in range(8, full, 8):
+            yield dict(kernel=_lib.KERNEL_MFMA_LDS, m_tiles=mt, n_tiles=nt, unroll=2, k_chunk=256, splits=sp,
+                       channels=ch)
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(1, 96, 1536, NONE), (13, 200, 1000, NONE), (40, 6144, 2560, NONE),
+                                       (64, 130, 520, NONE), (5, 2 * 96, 2560, SILU), (24, 2 * 200, 1032, SILU)])
+def test_lds_partial_channel_configs(device, M, N, K, epi):
+    """Blocks of fewer channels than their tiles (the rest padding, neither
+    loaded nor stored) give the oracle's results, with and without split K,
+    at N that is and is not a multiple of the channel count."""
+    x = R.randn_bf16((M, K), 8750 + M)
+    w = R.randn_bf16((N, K), 8751 + N, 0.02)
+    _run_configs(x, w, epi, _lds_channel_configs(M, epi == SILU))
 
 
 @pytest.mark.parametrize("kernel", [_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_VALU])
@@ -1038,6 +1063,7 @@ def test_select_ties_nan_and_configs(device, M, N, K):
                  for nt in (1, 2, 4) for wv in (1, 4, 8)]
     cfgs += [dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=nt, unroll=pf, k_chunk=256, splits=1)
              for nt in (2, 4) for pf in (2, 3)]
+    cfgs += [dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=2, unroll=2, k_chunk=256, splits=1, channels=24)]
     cfgs += [dict(kernel=_lib.KERNEL_STREAM), dict(kernel=_lib.KERNEL_VALU, splits=2),
              dict(kernel=_lib.KERNEL_MFMA, splits=1)]
     base = {}
