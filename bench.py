@@ -299,16 +299,8 @@ def main() -> int:
                 row = {"shape": name, "M": Mt, "us": round(fused_ms * 1000, 2),
                        "prologue_kernel_plus_gemm_us": round(two_ms * 1000, 2),
                        "one_launch": G.normed_fused(Mt, Nw, K, G.EPILOGUE_SILU_MUL if silu else G.EPILOGUE_NONE)}
-                # Stream plans can also compute the prologue inside the kernel
-                # (prologue = 1, one launch); timed beside the plan.
-                inner = dict(op.resolved_config, prologue=1)
-                if op.resolved_config["kernel"] == 5 and G.normed_fused(Mt, Nw, K, op.epilogue, inner):
-                    op1 = (G.SkinnyGateUp(Mt, Nw // 2, K, dev, config=inner) if silu
-                           else G.SkinnyMatmul(Mt, Nw, K, dev, config=inner))
-                    one_ms = replay_ms([(lambda w=ws[i % len(ws)]: op1.run(xt, w, ot, norm=(yt, wn, xo, eps)))
-                                        for i in range(n)])
-                    row["in_kernel_prologue_us"] = round(one_ms * 1000, 2)
-                    del op1
+                row["plain_gemm_us"] = round(replay_ms([(lambda w=ws[i % len(ws)]: op.run(xt, w, ot))
+                                                        for i in range(n)]) * 1000, 2)
                 if not args.no_torch:
                     def torch_normed(w):
                         s_ = (xt.float() + yt.float()).to(torch.bfloat16)
@@ -321,8 +313,7 @@ def main() -> int:
                     row["torch_gpu_us"] = round(tms * 1000, 2)
                 normed.append(row)
                 log(f"normed M={Mt:3d} {name:8s} {row['us']:8.2f} us ({'1 launch' if row['one_launch'] else '2 launches'})"
-                    f"   prologue+gemm {row['prologue_kernel_plus_gemm_us']:8.2f} us"
-                    + (f"   in-kernel prologue {row['in_kernel_prologue_us']:8.2f} us" if "in_kernel_prologue_us" in row else "")
+                    f"   prologue+gemm {row['prologue_kernel_plus_gemm_us']:8.2f} us   plain gemm {row['plain_gemm_us']:8.2f} us"
                     + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
 
     # ------------------------------------------------------------ token selection

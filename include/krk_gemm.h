@@ -118,12 +118,11 @@ typedef struct krk_gemm_config {
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
     int k_chunk;  /* MFMA_LDS: k per pipeline stage, 256 or 512 (512 needs
                      m_tiles + n_tiles <= 4); other kernels: ignored */
-    int prologue; /* normed calls (krk_gemm_bf16_normed_config): 0 = the plan's way
-                     (a separate prologue kernel, or inside the VALU kernel at
-                     M = 1); 1 = inside a STREAM kernel at any M, computed by
-                     producer waves and handed to the other workgroups through
-                     the workspace (K <= 4096, at most 5 K stages per split).
-                     Ignored by plain calls. */
+    int prologue; /* normed calls (krk_gemm_bf16_normed_config): 0 = fused into
+                     the projection kernel where the configuration allows it
+                     (krk_gemm_normed_fused), else a separate prologue kernel;
+                     1 = always the separate prologue kernel.  Ignored by
+                     plain calls. */
     int channels; /* MFMA_LDS: output channels per workgroup, a multiple of 8 up
                      to 16·n_tiles (8·n_tiles with SILU_MUL); 0 = all of them.
                      Fewer channels than the tiles hold leave the rest of the
@@ -209,12 +208,15 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx,
  *              its split-K counters must be zero before first use (every call
  *              leaves them zero); the rest is scratch.
  *
- * At M = 1, VALU plans of at most 2048 workgroups run the prologue inside the
- * projection kernel (one launch); so do STREAM configurations with
- * prologue = 1 at any M (krk_gemm_normed_fused tells which).  Other calls run
- * a one-workgroup-per-row prologue kernel that writes xout and the
- * normalised rows into the workspace, then the projection: measured faster
- * than the in-kernel hand-off at M >= 2, so the plan uses it there.
+ * Fused (one launch; krk_gemm_normed_fused tells when): a VALU
+ * configuration, K unsplit, at the depth that covers K = 2560 in one pass,
+ * with a wave per 512-k block (K <= 512·waves).  Every workgroup then
+ * normalises the rows of x itself while its first weight loads are in
+ * flight (no workgroup waits for another; workgroup 0 writes xout).
+ * Otherwise (and with prologue = 1) a one-workgroup-per-row prologue kernel
+ * writes xout and the normalised rows into the workspace, then the
+ * projection runs.  Both use the rounding points above.  With cfg == NULL
+ * the call uses krk_gemm_normed_plan.
  */
 int krk_gemm_bf16_normed(const void* x, int64_t ldx, const void* d, int64_t ldd,
                          const void* w_norm, float eps, void* xout, int64_t ldxo,
@@ -233,10 +235,18 @@ int krk_gemm_bf16_normed_config(const void* x, int64_t ldx, const void* d, int64
  * plan).  0 for an invalid shape or configuration. */
 size_t krk_gemm_normed_workspace_bytes(int M, int N, int K, int epilogue, const krk_gemm_config* cfg);
 
-/* 1 when the normed call for this shape and configuration (NULL = the plan)
- * runs the prologue inside the projection kernel, 0 when it launches the
- * separate prologue kernel first, negative on an invalid shape/config. */
+/* 1 when the normed call for this shape and configuration (NULL = the
+ * normed plan) runs the prologue inside the projection kernel, 0 when it
+ * launches the separate prologue kernel first, negative on an invalid
+ * shape/config. */
 int krk_gemm_normed_fused(int M, int N, int K, int epilogue, const krk_gemm_config* cfg);
+
+/* The configuration krk_gemm_bf16_normed uses (the normed plan): fused where
+ * that measured fastest (qkv at M <= 4, gate_up and lm_head at M <= 2 of
+ * Qwen3-4B), else the plain plan with prologue = 1.  Like krk_gemm_plan it
+ * replaces the configuration pick_normed settles on
+ * (engine/kernels/gemm.py:501-560).  KRK_OK or a negative code. */
+int krk_gemm_normed_plan(int M, int N, int K, int epilogue, krk_gemm_config* out);
 
 /*
  * krk_add_rms_norm_bf16 — the stand-alone prologue: xout = bf16(x + d) and

@@ -568,10 +568,9 @@ int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int XS, bool SILU, int SK = 0, bool NORM = false>
-int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {},
-                  krk::CoopNorm cn = {}) {
-    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK, NORM>);
+template <int MT, int XS, bool SILU, int SK = 0>
+int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {}) {
+    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK>);
     int nred = stream_nred_for(a.K, a.splits);
     size_t shm = krk::stream_lds_bytes(MT, depth, nred);
     const int G = stream_groups(nblocks, a.splits);
@@ -592,7 +591,7 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     const int groups = G * a.splits;
     void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w, (void*)&a.ldw, (void*)&a.y, (void*)&a.ldy,
                     (void*)&a.M, (void*)&a.N,   (void*)&a.K, (void*)&a.splits, (void*)&depth, (void*)&obcap,
-                    (void*)&nred, (void*)&a.part, (void*)&a.ctr, (void*)&sa, (void*)&cn};
+                    (void*)&nred, (void*)&a.part, (void*)&a.ctr, (void*)&sa};
     hipError_t e = hipLaunchKernel(fn, dim3(groups), dim3(64 * krk::kStreamWaves), args, shm, stream);
     return hip_status(e, "stream_gemm_kernel launch");
 }
@@ -642,31 +641,6 @@ int dispatch_stream_sel(const LaunchArgs& a, const krk_gemm_config& c, int nbloc
         }
     }
     return fail(KRK_ERR_UNSUPPORTED, "STREAM selection epilogue: m_tiles=%d", c.m_tiles);
-}
-
-// Normed stream calls compute the RMSNorm prologue in the kernel
-// (krk_coop.h); instantiated for a split's K range of 4 or 5 stages (K up
-// to 2560, the hidden size every normed projection reads).
-template <int MT, bool SILU>
-int dispatch_stream_norm_xs(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
-                            const krk::CoopNorm& cn) {
-    switch (stream_xs(MT, cdiv(cdiv(a.K, krk::kStreamKC), c.splits))) {
-        case 4: return launch_stream<MT, 4, SILU, 0, true>(a, nblocks, c.unroll, s, {}, cn);
-        case 5: return launch_stream<MT, 5, SILU, 0, true>(a, nblocks, c.unroll, s, {}, cn);
-    }
-    return fail(KRK_ERR_UNSUPPORTED, "STREAM normed: no instantiation for m_tiles=%d and this K split", MT);
-}
-
-template <bool SILU>
-int dispatch_stream_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
-                         const krk::CoopNorm& cn) {
-    switch (c.m_tiles) {
-        case 1: return dispatch_stream_norm_xs<1, SILU>(a, c, nblocks, s, cn);
-        case 2: return dispatch_stream_norm_xs<2, SILU>(a, c, nblocks, s, cn);
-        case 3: return dispatch_stream_norm_xs<3, SILU>(a, c, nblocks, s, cn);
-        case 4: return dispatch_stream_norm_xs<4, SILU>(a, c, nblocks, s, cn);
-    }
-    return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
 
 template <bool SILU>
@@ -766,60 +740,61 @@ int dispatch_valu_norm_r(const LaunchArgs& a, const krk_gemm_config& c, int nblo
 template <bool SILU>
 int dispatch_valu_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
                        const krk::NormArgs& na) {
-    if (c.m_tiles == 1) return dispatch_valu_norm_r<1, SILU>(a, c, nblocks, s, na);
-    return fail(KRK_ERR_UNSUPPORTED, "the fused prologue runs at M = 1, got %d x rows", c.m_tiles);
+    switch (c.m_tiles) {
+        case 1: return dispatch_valu_norm_r<1, SILU>(a, c, nblocks, s, na);
+        case 2: return dispatch_valu_norm_r<2, SILU>(a, c, nblocks, s, na);
+        case 4: return dispatch_valu_norm_r<4, SILU>(a, c, nblocks, s, na);
+        case 8: return dispatch_valu_norm_r<8, SILU>(a, c, nblocks, s, na);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "VALU normed: x rows=%d", c.m_tiles);
 }
 
-// The fused prologue makes every workgroup stage x and d for the whole K and
-// take the row statistics itself.  Measured on MI355X, that pays only when it
-// is small next to the workgroup's share of W: at M = 1 with at most
-// kNormFusedMaxGroups workgroups (qkv 8.9 vs 9.7 us, gate_up 19.0 vs 19.7 us
-// against the prologue kernel + projection).  lm_head's 19k workgroups lose
-// 15 us at M = 1, and at M = 4..8 the staging rivals the weight stream
-// (gate_up M = 8: 115 vs 23 us), so those run the separate prologue kernel.
-constexpr int kNormFusedMaxGroups = 2048;
-
-// Whether a resolved configuration runs the RMSNorm prologue inside the VALU
-// kernel (else a separate prologue kernel writes the normalised rows first).
-// Fault injection for tests of the in-kernel prologue's bounded wait:
-// KRK_COOP_PRODUCERS=0 turns the producer waves off (every workgroup then
-// times out and computes the rows itself) and KRK_COOP_WAIT_US sets the bound
-// of the wait (default 30 us).  Read at every call.
-int coop_producers_enabled() {
-    const char* e = getenv("KRK_COOP_PRODUCERS");
-    return (e && e[0] == '0' && e[1] == '\0') ? 0 : 1;
-}
-uint32_t coop_wait_ticks() {
-    const char* e = getenv("KRK_COOP_WAIT_US");
-    if (!e || !*e) return krk::kCoopWaitTicks;
-    const long us = strtol(e, nullptr, 10);
-    return us >= 1 && us <= 1000000 ? (uint32_t)(us * 100) : krk::kCoopWaitTicks;
-}
-
-// Whether a STREAM configuration can compute the prologue in the kernel
-// (krk_coop.h): instantiated for up to 5 K stages per split.
-bool coop_capable(int K, const krk_gemm_config& c) {
-    if (c.kernel != KRK_KERNEL_STREAM || K > krk::kCoopMaxK) return false;
-    const int xs = stream_xs(c.m_tiles, cdiv(cdiv(K, krk::kStreamKC), c.splits));
-    return xs == 4 || xs == 5;
-}
-
-// In-kernel prologue: asked for by the configuration (prologue = 1).  The
-// plan never asks: at gate_up M = 32 the hand-off took the stream kernel
-// from 23.5 to 33.5 us against 27.2 us for the prologue kernel + projection
-// (producer loads ~2 us, their stores ~2.5 us, the flag's trip through
-// device-coherent memory and the polls 1.5-3 us; measured per workgroup).
-bool norm_coop(int M, int K, const krk_gemm_config& c) {
-    (void)M;
-    return c.prologue == 1 && coop_capable(K, c);
-}
-
+// Whether a resolved configuration fuses the RMSNorm prologue into the
+// projection kernel (one launch), else a separate prologue kernel writes the
+// normalised rows first (also what prologue = 1 asks for).  Both keep the
+// reference's rounding points (krk_norm.h).  Fused: a VALU configuration,
+// K unsplit, at the depth covering K = 2560, with a wave per 512-k block.
+//
+// Every workgroup of a fused call normalises all M rows itself (about ten
+// VALU instructions per element), so the fused form pays only at small M:
+// measured on MI355X, normed qkv / gate_up / lm_head at M = 1 take 7.2 /
+// 16.8 / 106.9 us fused against 9.7 / 19.6 / 110.6 us behind the prologue
+// kernel, while at M = 4 gate_up takes 22.7 us fused against 20.6 us.  (A
+// fused form of the persistent stream kernel never beat the prologue kernel:
+// each of its 256 workgroups normalises every row, ~3 us per 16 rows of
+// VALU work ahead of the first MFMA.)
 bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
-    if (norm_coop(M, K, c)) return true;
-    if (c.kernel != KRK_KERNEL_VALU || M != 1 || c.unroll != kValuNormDepth) return false;
-    const Geometry g = geometry(M, N, epilogue, c);
-    return (int64_t)g.nblocks * c.splits <= kNormFusedMaxGroups &&
-           krk::valu_norm_lds_bytes(c.m_tiles, cdiv(K, krk::kValuBlock)) <= kLdsMax;
+    (void)M;
+    (void)N;
+    (void)epilogue;
+    if (c.prologue != 0 || c.splits != 1 || c.kernel != KRK_KERNEL_VALU) return false;
+    const int nb = cdiv(K, krk::kValuBlock);
+    return c.unroll == kValuNormDepth && nb <= c.waves && krk::valu_norm_lds_bytes(c.m_tiles, nb) <= kLdsMax;
+}
+
+// Plans of the normed calls (cfg == NULL): fused configurations where they
+// measured fastest (tuner, graph replay over rotating weights, MI355X); every
+// other shape and M runs its plain plan behind the prologue kernel.
+const TableEntry kNormTable[] = {
+    {6144, 2560, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_VALU, 4, 5, 8, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 5, 8, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
+};
+
+int normed_plan(int M, int N, int K, int epilogue, krk_gemm_config* out) {
+    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
+    for (const TableEntry& e : kNormTable)
+        if (e.N == N && e.K == K && e.epilogue == epilogue && Mc >= e.m_lo && Mc <= e.m_hi)
+            return resolve_config(M, N, K, epilogue, &e.cfg, out);
+    const int rc = resolve_config(M, N, K, epilogue, nullptr, out);
+    if (rc == KRK_OK) out->prologue = 1;
+    return rc;
+}
+
+// A normed call's configuration: the caller's, else the normed plan.
+int resolve_normed(int M, int N, int K, int epilogue, const krk_gemm_config* cfg, krk_gemm_config* out) {
+    return cfg ? resolve_config(M, N, K, epilogue, cfg, out) : normed_plan(M, N, K, epilogue, out);
 }
 
 // The residual-add + RMSNorm prologue of a normed call (krk_norm.h).
@@ -835,24 +810,16 @@ struct NormSpec {
 // Workspace of a call: [split-K counters and partials][normalised rows
 // M x K bf16 when a separate prologue writes them].
 struct WorkspaceLayout {
-    size_t gemm;         // split-K part, at offset 0
-    size_t n_off;        // offset of the normalised rows, or of the in-kernel prologue's control block (0 if none)
-    size_t coop_copies;  // offset of the in-kernel prologue's per-die copies (0 if none)
-    int64_t slot_elems;  // elements per copy
+    size_t gemm;   // split-K part, at offset 0
+    size_t n_off;  // offset of the normalised rows (0 if none)
     size_t total;
 };
 WorkspaceLayout workspace_layout(int M, int N, int K, int epilogue, const krk_gemm_config& c, bool normed) {
     WorkspaceLayout l;
     l.gemm = workspace_for(M, N, epilogue, c);
     const bool prologue = normed && !norm_fused(M, N, K, epilogue, c);
-    const bool coop = normed && norm_coop(M, K, c);
-    l.n_off = (prologue || coop) ? align_up(l.gemm, 256) : 0;
-    l.coop_copies = coop ? l.n_off + align_up(krk::coop_ctl_bytes(), 256) : 0;
-    const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
-    l.slot_elems = coop ? (int64_t)(krk::coop_slot_bytes(Mc, K, c.m_tiles) / sizeof(uint16_t)) : 0;
-    l.total = prologue ? l.n_off + (size_t)M * K * sizeof(uint16_t)
-              : coop   ? l.coop_copies + krk::coop_copy_bytes(Mc, K, c.m_tiles)
-                       : l.gemm;
+    l.n_off = prologue ? align_up(l.gemm, 256) : 0;
+    l.total = prologue ? l.n_off + (size_t)M * K * sizeof(uint16_t) : l.gemm;
     return l;
 }
 
@@ -891,7 +858,7 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     }
 
     krk_gemm_config c;
-    rc = resolve_config(M, N, K, epilogue, cfg, &c);
+    rc = ns ? resolve_normed(M, N, K, epilogue, cfg, &c) : resolve_config(M, N, K, epilogue, cfg, &c);
     if (rc) return rc;
 
     const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((uint64_t)(M - 1) * ldx + K) * 2;
@@ -935,7 +902,6 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     if (ns) na = krk::NormArgs{static_cast<const uint16_t*>(ns->d), ns->ldd, static_cast<const uint16_t*>(ns->w_norm),
                                ns->eps, static_cast<uint16_t*>(ns->xout), ns->ldxo};
     const bool fused = ns && norm_fused(M, N, K, epilogue, c);
-    const bool coop = ns && norm_coop(M, K, c);
     // Projection input: x itself, or the normalised rows a prologue kernel
     // writes into the workspace.
     const uint16_t* xin = static_cast<const uint16_t*>(x);
@@ -965,25 +931,12 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
         a.part = part;
         a.ctr = ctr;
         a.cb = g.cb;
-        if (fused && coop) {
-            // This chunk's rows of x, d and xout; the control block and the
-            // copies are reused by the chunks in stream order.
-            krk::CoopNorm cn;
-            cn.x = static_cast<const uint16_t*>(x) + (int64_t)m0 * ldx;
-            cn.ldx = ldx;
-            cn.na = na;
-            cn.na.d += (int64_t)m0 * na.ldd;
-            cn.na.xout += (int64_t)m0 * na.ldxo;
-            cn.ctl = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + wl.n_off);
-            cn.copies = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + wl.coop_copies);
-            cn.slot_elems = wl.slot_elems;
-            cn.M = a.M;
-            cn.K = K;
-            cn.producers = coop_producers_enabled();
-            cn.wait_ticks = coop_wait_ticks();
-            rc = silu ? dispatch_stream_norm<true>(a, c, g.nblocks, st, cn) : dispatch_stream_norm<false>(a, c, g.nblocks, st, cn);
-        } else if (fused) {
-            rc = silu ? dispatch_valu_norm<true>(a, c, g.nblocks, st, na) : dispatch_valu_norm<false>(a, c, g.nblocks, st, na);
+        if (fused) {
+            // This chunk's rows of d and xout.
+            krk::NormArgs nc = na;
+            nc.d += (int64_t)m0 * na.ldd;
+            nc.xout += (int64_t)m0 * na.ldxo;
+            rc = silu ? dispatch_valu_norm<true>(a, c, g.nblocks, st, nc) : dispatch_valu_norm<false>(a, c, g.nblocks, st, nc);
         } else if (c.kernel == KRK_KERNEL_MFMA) {
             rc = silu ? dispatch_mfma<true>(a, c, g.nblocks, st) : dispatch_mfma<false>(a, c, g.nblocks, st);
         } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {
@@ -1299,7 +1252,7 @@ int krk_gemm_bf16_normed_config(const void* x, int64_t ldx, const void* d, int64
 size_t krk_gemm_normed_workspace_bytes(int M, int N, int K, int epilogue, const krk_gemm_config* cfg) {
     if (check_shape(M, N, K, epilogue)) return 0;
     krk_gemm_config c;
-    if (resolve_config(M, N, K, epilogue, cfg, &c)) return 0;
+    if (resolve_normed(M, N, K, epilogue, cfg, &c)) return 0;
     return workspace_layout(M, N, K, epilogue, c, true).total;
 }
 
@@ -1308,8 +1261,16 @@ int krk_gemm_normed_fused(int M, int N, int K, int epilogue, const krk_gemm_conf
     int rc = check_shape(M, N, K, epilogue);
     if (rc) return rc;
     krk_gemm_config c;
-    if ((rc = resolve_config(M, N, K, epilogue, cfg, &c))) return rc;
+    if ((rc = resolve_normed(M, N, K, epilogue, cfg, &c))) return rc;
     return norm_fused(M, N, K, epilogue, c) ? 1 : 0;
+}
+
+int krk_gemm_normed_plan(int M, int N, int K, int epilogue, krk_gemm_config* out) {
+    g_err[0] = '\0';
+    int rc = check_shape(M, N, K, epilogue);
+    if (rc) return rc;
+    if (!out) return fail(KRK_ERR_INVALID, "null output configuration");
+    return normed_plan(M, N, K, epilogue, out);
 }
 
 int krk_add_rms_norm_bf16(const void* x, int64_t ldx, const void* d, int64_t ldd, const void* w_norm, float eps,

@@ -14,6 +14,11 @@
 // plus eps.  Sums of squares are taken in a fixed order (per thread in k
 // order, then a fixed butterfly, then waves in order), so results are
 // deterministic.
+//
+// The projection kernels fuse the prologue with these same rounding points:
+// each wave of a workgroup owns whole x rows (every k), so it takes a row's
+// statistic with a wave butterfly and normalises the row itself before the
+// projection consumes it; no workgroup waits for another.
 #pragma once
 
 #include "krk_common.h"
@@ -67,6 +72,53 @@ __device__ __forceinline__ u32x4 normalize_bf16x8(const u32x4& s, float rstd, co
         r[j] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
     }
     return r;
+}
+
+// Two fp32 values -> packed bf16 bits (lo in bits 0-15), round to nearest
+// even by gfx950's v_cvt_pk_bf16_f32 (the same bits as f32_to_bf16 for every
+// non-NaN input; a NaN stays a NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2 v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// s = bf16(x + d) for 8 elements; ss += Σ s² (two squares per v_dot2: exact
+// bf16 products, fp32 sums, in element order).
+__device__ __forceinline__ u32x4 add_sumsq_bf16x8(const u32x4& x, const u32x4& d, float& ss) {
+    u32x4 s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // Through a scalar: clang reads a vector-element operand of
+        // __builtin_bit_cast as element 0 (seen in the gfx950 code).
+        const uint32_t sj = pack_bf16x2(bf16_to_f32(x[j] & 0xffffu) + bf16_to_f32(d[j] & 0xffffu),
+                                        bf16_to_f32(x[j] >> 16) + bf16_to_f32(d[j] >> 16));
+        const bf16x2 sp = __builtin_bit_cast(bf16x2, sj);
+        ss = __builtin_amdgcn_fdot2_f32_bf16(sp, sp, ss, false);
+        s[j] = sj;
+    }
+    return s;
+}
+
+// n = bf16(bf16(s · rstd) · wn) for 8 elements (hardware conversions).
+__device__ __forceinline__ u32x4 normalize_hw_bf16x8(const u32x4& s, float rstd, const u32x4& wn) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t nj = pack_bf16x2(bf16_to_f32(s[j] & 0xffffu) * rstd, bf16_to_f32(s[j] >> 16) * rstd);
+        r[j] = pack_bf16x2(bf16_to_f32(nj & 0xffffu) * bf16_to_f32(wn[j] & 0xffffu),
+                           bf16_to_f32(nj >> 16) * bf16_to_f32(wn[j] >> 16));
+    }
+    return r;
+}
+
+// Σ over the wave of a per-lane value, the same in every lane: a fixed xor
+// butterfly, then lane 0's sum broadcast.
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
 __device__ __forceinline__ float rms_rstd(float sumsq, int K, float eps) {

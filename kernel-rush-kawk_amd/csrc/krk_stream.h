@@ -32,7 +32,6 @@
 // reduced through LDS in fixed wave order.
 #pragma once
 
-#include "krk_coop.h"
 #include "krk_epilogue.h"
 #include "krk_select.h"
 #include "krk_sync.h"
@@ -63,44 +62,22 @@ __host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth, int nre
 // blocks, [slot][16·MT rows][CB channels].
 __host__ __device__ constexpr size_t stream_out_bytes(int MT, bool silu) { return (size_t)(silu ? 8 : 16) * 16 * MT * 2; }
 
-// Copy layout of the normed kernel's rows (krk_coop.h): x as this kernel's
-// MFMA A fragments, [512-k stage j][wave w][k-step kk][m tile i][lane] x 16
-// bytes, lane (r, q) holding x[16i + r][512j + 32(KPW·w + kk) + 8q .. +7], so
-// each wave loads its fragments as contiguous 1 KB pieces straight from its
-// die's L2 (no trip through LDS).
-template <int MT>
-struct StreamFragLayout {
-    uint16_t* base;
-    __device__ __forceinline__ uint16_t* at(int m, int k) const {
-        const int j = k >> 9, ks = (k >> 5) & 15, q = (k >> 3) & 3;
-        const int w = ks / kStreamKPW, kk = ks % kStreamKPW;
-        const int i = m >> 4, r = m & 15;
-        return base + ((int64_t)(((j * kStreamWaves + w) * kStreamKPW + kk) * MT + i) * 64 + r + 16 * q) * 8;
-    }
-};
-
 // MT: 16-row m tiles (M <= 16·MT).  XS: most K stages a workgroup owns (its
 // x fragments live in X[XS][2][MT]).  SILU: gate/up blocks with the epilogue.
 // SK (K unsplit): 1 or kSelMaxK — each workgroup keeps every row's SK
 // largest (value, index) keys over its blocks (krk_select.h) and writes them
 // to sa.keys[m][workgroup * SK ...]; y (the logits) is written only when
 // non-null.  0: no selection.
-// NORM: x is rms_norm(cn.x + cn.na.d) computed in the kernel (krk_coop.h):
-// the workgroups at the end of each die's order produce the rows (one per
-// wave) into their die's copy in fragment layout (StreamFragLayout), and
-// every workgroup reads its x fragments from there.  The x argument is
-// unused.
-template <int MT, int XS, bool SILU, int SK = 0, bool NORM = false>
+template <int MT, int XS, bool SILU, int SK = 0>
 __global__ void __launch_bounds__(512)
 stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                    const uint16_t* __restrict__ w, int64_t ldw,
                    uint16_t* __restrict__ y, int64_t ldy,
                    int M, int N, int K, int splits, int depth, int obcap, int nred,
-                   float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa, CoopNorm cn) {
+                   float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa) {
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     constexpr bool SEL = SK > 0;
     static_assert(!(SEL && SILU), "selection reads plain logits");
-    static_assert(!(SEL && NORM), "the normed lm_head selects through its own call");
     static_assert(SK == 0 || SK == 1 || SK == kSelMaxK, "argmax or top-kSelMaxK");
     constexpr int WV = kStreamWaves;
     constexpr int KPW = kStreamKPW;
@@ -159,38 +136,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     // x fragments X[j][kk][i] of the workgroup's K stages: lane (r, q) =
     // x[16i + r][32·(KPW·wave + kk) + 8q .. +7] of stage sb + j.
     u32x4 X[XS][KPW][MT];
-    [[maybe_unused]] CoopMarks marks{0, 0, 0};
-    [[maybe_unused]] __shared__ int coop_word;
-    if constexpr (NORM) {
-        // Normed calls: the producer waves compute their rows into their
-        // die's copy, in fragment layout, while the memory system is quiet
-        // (measured: behind the other workgroups' ring prologues every step
-        // of the hand-off was 2-4x slower); every workgroup waits for the
-        // rows, loads its fragments, and only then starts the ring.
-        marks.slot = coop_slot();
-        const StreamFragLayout<MT> copy{coop_copy(cn, marks.slot)};
-        const int p = coop_producer_index(blockIdx.x, gridDim.x, true);
-        if (p * WV < cn.M) coop_produce(cn, copy, marks, p, WV, wave, lane);
-        if (T > 0) issue(0);  // one stage only: a deeper start slows the hand-off (measured)
-        coop_wait(cn, copy, marks, wave, lane, WV, &coop_word);
-#pragma unroll
-        for (int j = 0; j < XS; ++j) {
-#pragma unroll
-            for (int kk = 0; kk < KPW; ++kk) {
-                const int k = (sb + j) * kStreamKC + 32 * (KPW * wave + kk) + 8 * q;
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    const bool ok = j < nst && 16 * i + r < M && k < K;
-                    const u32x4 v = 16 * i < M && j < nst ? load_cached16(copy.at(16 * i + r, (sb + j) * kStreamKC +
-                                                                                  32 * (KPW * wave + kk) + 8 * q))
-                                                          : u32x4{0u, 0u, 0u, 0u};
-                    X[j][kk][i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
-                }
-            }
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        for (int d = 1; d < depth - 1 && d < T; ++d) issue(d);
-    } else {
+    {
         // x for the workgroup's K range, loaded once.  Whole 1 KB row pieces (wave
         // w loads rows w, w + 8, ... of every stage): a CU pulls L2 data ~2.5x
         // faster this way than in the MFMA fragment pattern.  Rows past M, k past
@@ -384,7 +330,6 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             flush(base, myblocks - base);
         }
     }
-    if constexpr (NORM) coop_finish(cn, marks, lane);
     if constexpr (SEL) {
         // Reduce each row's keys over its 16 channels (lane bits 2..5: the
         // block size covers the items of one slot, so it and lane agree in

@@ -43,11 +43,10 @@ constexpr int kValuLdsMinRows = 4;  // x rows from which x is staged in LDS
 __host__ __device__ constexpr size_t valu_lds_bytes(int MX, int blocks) {
     return MX < kValuLdsMinRows ? 0 : (size_t)MX * blocks * kValuBlock * sizeof(uint16_t);
 }
-// With the fused RMSNorm prologue: x and the branch rows of the whole K
-// (nb blocks), the RMSNorm gain (nb blocks), then the per-wave partial sums
-// of squares.
+// With the fused RMSNorm prologue: the normalised rows of the whole K
+// (nb blocks), then the per-wave partial sums of squares.
 __host__ __device__ constexpr size_t valu_norm_lds_bytes(int MX, int nb) {
-    return (size_t)(2 * MX + 1) * nb * kValuBlock * sizeof(uint16_t) + (size_t)MX * kValuMaxWaves * sizeof(float);
+    return (size_t)MX * nb * kValuBlock * sizeof(uint16_t) + (size_t)MX * kValuMaxWaves * sizeof(float);
 }
 
 __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2, v); }
@@ -131,10 +130,12 @@ constexpr int log2_exact() {
 // matching R/2 up rows); D: 512-element blocks loaded per row before the wave
 // consumes them; EXACT: K is whole blocks and every split is whole chunks of D
 // blocks, so no load needs clamping and no lane masking.  NORM: x is the
-// residual stream and the projection input is rms_norm(x + na.d) (krk_norm.h):
-// every workgroup stages x and d for the whole K in LDS, takes the row
-// statistics, and replaces its split's x blocks by the normalised rows;
-// workgroup (0, 0) also writes na.xout.
+// residual stream and the projection input is rms_norm(x + na.d) with the
+// rounding points of krk_norm.h (K unsplit, one 512-k block per wave at
+// most): wave w takes block w of every row (x, d and the gain in 2·MX + 1
+// registers of 16 bytes, loaded before the first W loads), the row sums of
+// squares meet in LDS, and each wave writes its normalised block there while
+// the W loads are in flight; workgroup 0 also writes na.xout.
 // Grid: x = output blocks, y = K splits; blockDim = 64 x waves; each workgroup
 // covers waves * R (SILU: waves * R/2) consecutive output channels.  Split s
 // owns K blocks [s*per + min(s, rem), ...) where per = nb / splits and
@@ -255,9 +256,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
                 u32x4 xb[MX];
 #pragma unroll
                 for (int m = 0; m < MX; ++m) {
-                    if constexpr (NORM) {
-                        xb[m] = *reinterpret_cast<const u32x4*>(xs + ((size_t)(m * nb + bb) * kValuBlock + lane_k) * 2);
-                    } else if constexpr (XLDS) {
+                    if constexpr (XLDS) {
                         xb[m] = *reinterpret_cast<const u32x4*>(
                             xs + ((size_t)(m * (b1 - b0) + (bb - b0)) * kValuBlock + lane_k) * 2);
                     } else {
@@ -290,52 +289,32 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
     // usually one chunk.
     int b = b0;
     if constexpr (NORM) {
-        // x and d rows of the whole K into LDS as [m][block][512] (x, then d),
-        // and the gain as [block][512], one 1 KB DMA per (row, block); then
-        // the first W loads.  (A global load of the gain after the W loads
-        // would wait behind them: vmcnt retires in order.)
-        unsigned char* const ds = xs + (size_t)MX * nb * kValuBlock * 2;
-        unsigned char* const gs = ds + (size_t)MX * nb * kValuBlock * 2;
-        float* const red = reinterpret_cast<float*>(gs + (size_t)nb * kValuBlock * 2);
-        const uint16_t* drow[MX];
+        // Block bw = wave of every row (lane l: k = 512·bw + 8l); waves past
+        // the last block, and k past K, hold zeros.  Rows past M read row
+        // M - 1.
+        const int bw = wave;
+        const uint32_t k = (uint32_t)bw * kValuBlock + lane_k;
+        const bool kin = bw < nb && k < (uint32_t)K;
+        const uint32_t kc = kin ? k : 0u;
+        const u32x4 gv = load_row16(na.wn, 2u * kc);
+        u32x4 xr[MX], dr[MX];
 #pragma unroll
-        for (int m = 0; m < MX; ++m) drow[m] = na.d + (int64_t)(m < M ? m : M - 1) * na.ldd;
-        auto kfull = [&](int bb) -> uint32_t {
-            const uint32_t k = (uint32_t)bb * kValuBlock + lane_k;
-            return k < (uint32_t)K ? k : 0u;
-        };
-        for (int j = wave; j < 2 * MX * nb; j += waves) {
-            const int isd = j >= MX * nb;
-            const int jj = isd ? j - MX * nb : j;
-            const int m = jj / nb;
-            const int bb = jj - m * nb;
-            const uint16_t* src = (isd ? drow[m] : xrow[m]) + kfull(bb);
-            dma_row(src, (isd ? ds : xs) + (size_t)jj * (kValuBlock * 2));
+        for (int m = 0; m < MX; ++m) {
+            xr[m] = load_row16(xrow[m], 2u * kc);
+            dr[m] = load_row16(na.d + (int64_t)(m < M ? m : M - 1) * na.ldd, 2u * kc);
         }
-        for (int bb = wave; bb < nb; bb += waves) dma_row(na.wn + kfull(bb), gs + (size_t)bb * (kValuBlock * 2));
-        // The first W loads go out behind the DMAs, and (EXACT) only the DMAs
-        // are waited for: the statistics below overlap the weight stream.
         issue_first_chunk(b0);
-        bare_barrier();
-        // Sums of squares of s = bf16(x + d) per row; s replaces x in LDS.
+        // s = bf16(x + d) (workgroup 0 writes it to xout) and the wave's
+        // partial Σ s² per row, folded in fixed order.
         const bool write_xout = blockIdx.x == 0 && blockIdx.y == 0;
         float ss[MX];
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
             ss[m] = 0.0f;
-            for (int e = threadIdx.x; e < nb * 64; e += blockDim.x) {
-                const uint32_t k = 8u * (uint32_t)e;
-                if (k < (uint32_t)K) {
-                    unsigned char* px = xs + ((size_t)m * nb * kValuBlock + k) * 2;
-                    const u32x4 sv = add_bf16x8(*reinterpret_cast<const u32x4*>(px),
-                                                *reinterpret_cast<const u32x4*>(ds + ((size_t)m * nb * kValuBlock + k) * 2));
-                    *reinterpret_cast<u32x4*>(px) = sv;
-                    if (write_xout && m < M) *reinterpret_cast<u32x4*>(na.xout + (int64_t)m * na.ldxo + k) = sv;
-                    ss[m] = sumsq_bf16x8(sv, ss[m]);
-                }
-            }
+            xr[m] = add_sumsq_bf16x8(kin ? xr[m] : u32x4{0u, 0u, 0u, 0u}, kin ? dr[m] : u32x4{0u, 0u, 0u, 0u}, ss[m]);
+            if (write_xout && kin && m < M) *reinterpret_cast<u32x4*>(na.xout + (int64_t)m * na.ldxo + k) = xr[m];
         }
-        // Fixed-order reduction: butterfly within the wave, waves in order.
+        float* const red = reinterpret_cast<float*>(xs + (size_t)MX * nb * kValuBlock * 2);
         constexpr int PM = log2_exact<MX>();
         wave_fold<MX, 32>(ss, lane);
         {
@@ -344,27 +323,19 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
         }
         lds_wait();
         bare_barrier();
-        float rstd[MX];
+        // Row statistics (waves in order), then block bw of each row.
+        if (bw < nb) {
 #pragma unroll
-        for (int m = 0; m < MX; ++m) {
-            float t = red[m];
-            for (int wv = 1; wv < waves; ++wv) t += red[wv * MX + m];
-            rstd[m] = rms_rstd(t, K, na.eps);
-        }
-        // Normalise this split's blocks in place.
-        for (int e = threadIdx.x; e < (b1 - b0) * 64; e += blockDim.x) {
-            const uint32_t k = (uint32_t)b0 * kValuBlock + 8u * (uint32_t)e;
-            if (k < (uint32_t)K) {
-                const u32x4 g = *reinterpret_cast<const u32x4*>(gs + (size_t)k * 2);
-#pragma unroll
-                for (int m = 0; m < MX; ++m) {
-                    unsigned char* px = xs + ((size_t)m * nb * kValuBlock + k) * 2;
-                    *reinterpret_cast<u32x4*>(px) = normalize_bf16x8(*reinterpret_cast<const u32x4*>(px), rstd[m], g);
-                }
+            for (int m = 0; m < MX; ++m) {
+                float t = red[m];
+                for (int wv = 1; wv < waves; ++wv) t += red[wv * MX + m];
+                const float rstd = rms_rstd(t, K, na.eps);
+                *reinterpret_cast<u32x4*>(xs + ((size_t)(m * nb + bw) * kValuBlock + lane_k) * 2) =
+                    normalize_hw_bf16x8(xr[m], rstd, gv);
             }
         }
         lds_wait();
-        bare_barrier();
+        bare_barrier();  // publishes the normalised rows
         consume(b0);
         b += D;
     } else if constexpr (XLDS) {

@@ -86,6 +86,7 @@ SIGNATURES = {
                                             ctypes.POINTER(GemmConfig), _c_void_p, _size, _c_void_p]),
     "krk_gemm_normed_workspace_bytes": (_size, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_gemm_normed_fused": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
+    "krk_gemm_normed_plan": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig)]),
     "krk_add_rms_norm_bf16": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, ctypes.c_float, _c_void_p, _i64,
                                       _c_void_p, _i64, _int, _int, _c_void_p]),
     "krk_gemm_bf16_select": (_int, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _int, _int, _int, _int,

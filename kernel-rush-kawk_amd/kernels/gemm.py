@@ -36,7 +36,7 @@ from ._lib import EPILOGUE_NONE, EPILOGUE_SILU_MUL, GemmConfig
 
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "SkinnySelect", "pick_matmul", "pick_gateup", "pick_normed",
-    "add_rms_norm", "gemm_noalloc", "plan", "resolve", "config_from_triton", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
+    "add_rms_norm", "gemm_noalloc", "plan", "normed_plan", "resolve", "config_from_triton", "select_plan", "select_fused", "gemm_into", "normed_fused", "tune_projection", "_time",
 ]
 
 
@@ -44,6 +44,15 @@ def plan(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE) -> dict:
     """The configuration the library's dispatch table uses for this shape."""
     cfg = GemmConfig()
     _lib.check(_lib.load().krk_gemm_plan(M, N, K, epilogue, ctypes.byref(cfg)))
+    return cfg.as_dict()
+
+
+def normed_plan(M: int, N: int, K: int, epilogue: int = EPILOGUE_NONE) -> dict:
+    """The configuration a normed call of this shape uses without one (fused
+    where that measured fastest, else the plain plan behind the prologue
+    kernel, ``prologue = 1``)."""
+    cfg = GemmConfig()
+    _lib.check(_lib.load().krk_gemm_normed_plan(M, N, K, epilogue, ctypes.byref(cfg)))
     return cfg.as_dict()
 
 
@@ -492,14 +501,15 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
             return ok, why
     extra = []
     if norm is not None:
-        # Stream configurations can also compute the prologue in the kernel
-        # (prologue = 1); timed as whole normed calls like every candidate.
+        # A configuration that fuses the prologue into the projection is also
+        # timed behind the separate prologue kernel (prologue = 1); both are
+        # whole normed calls, like every candidate.
         for cfg in tune.candidates(M, N, K, epilogue):
-            if cfg["kernel"] == _lib.KERNEL_STREAM and normed_fused(M, N, K, epilogue, dict(cfg, prologue=1)):
+            if normed_fused(M, N, K, epilogue, cfg):
                 extra.append(dict(cfg, prologue=1))
     timer = lambda fn, rot_: _time(fn, rotate=rot_)
     return tune.search(kind, M, N, K, epilogue, a.device, build, accept, timer, rot, log=log, cache=cache, limit=limit,
-                       extra=extra)
+                       extra=extra, plan=normed_plan(M, N, K, epilogue) if norm is not None else None)
 
 
 def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = None, tune: bool = True, cache=None):

@@ -160,14 +160,16 @@ def close_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
 
 def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, accept, timer, rot: list,
            log=None, cache: TuneCache | None = None, limit: int | None = None,
-           extra: list | None = None) -> Result:
+           extra: list | None = None, plan: dict | None = None) -> Result:
     """Tune one shape.
 
     build(cfg) -> fn(w) runs the candidate on weight w and returns its output;
     accept(fn) -> (ok, text) validates one call; timer(fn, rot) -> ms per call.
-    The candidates are the library's (:func:`candidates`) followed by
-    ``extra``.  The plan (first candidate) is always measured; the rest while
-    the budget lasts (at most ``limit`` candidates in all when given)."""
+    The candidates are the library's (:func:`candidates`, led by the plan)
+    followed by ``extra``; ``plan`` replaces the library's plan at the head
+    (the normed calls' own plan).  The plan (first candidate) is always
+    measured; the rest while the budget lasts (at most ``limit`` candidates
+    in all when given)."""
     key = TuneCache.key(device, kind, M, N, K) if cache is not None else None
     if cache is not None:
         hit = cache.get(key)
@@ -176,6 +178,8 @@ def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, acce
                 log(f"tune {kind} M={M} N={N} K={K}: cached krk{hit}")
             return Result(hit, float("nan"), None, cached=True)
     cands = candidates(M, N, K, epilogue) + list(extra or [])
+    if plan is not None:
+        cands = [plan] + [c for c in cands if c != plan]
     if limit is not None:
         cands = cands[:max(1, limit)]
     trials: list[Trial] = []

@@ -266,45 +266,56 @@ def test_normed_argument_errors(lib, kw, code, msg):
 
 
 def test_normed_fused_plans(lib):
-    """The plans fuse the prologue at M = 1 on VALU plans of up to 2048
-    workgroups (qkv, gate_up); elsewhere they run the separate prologue
-    kernel first.  A stream configuration with prologue = 1 computes it in
-    the kernel at any M."""
-    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["gate_up"], 1, 1), (QWEN["qkv"], 4, 0),
-                                  (QWEN["gate_up"], 8, 0), (QWEN["lm_head"], 1, 0), (QWEN["qkv"], 32, 0),
-                                  (QWEN["gate_up"], 32, 0), (QWEN["lm_head"], 64, 0)]:
+    """The normed plans fuse the prologue into the VALU kernel where that
+    measured fastest (qkv at M <= 4, gate_up and lm_head at M <= 2) and
+    otherwise run the plain plan behind the separate prologue kernel
+    (prologue = 1).  A VALU configuration fuses when K is unsplit, the depth
+    covers K = 2560 and there is a wave per 512-k block; prologue = 1, split
+    K and the MFMA kernels never fuse."""
+    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["qkv"], 4, 1), (QWEN["qkv"], 8, 0),
+                                  (QWEN["gate_up"], 1, 1), (QWEN["gate_up"], 2, 1), (QWEN["gate_up"], 8, 0),
+                                  (QWEN["lm_head"], 1, 1), (QWEN["lm_head"], 2, 1), (QWEN["lm_head"], 4, 0),
+                                  (QWEN["gate_up"], 32, 0), (QWEN["qkv"], 32, 0), (QWEN["lm_head"], 64, 0)]:
         assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == fused, (N, M)
-    coop = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1)
-    for (N, K, epi), M in [(QWEN["gate_up"], 9), (QWEN["gate_up"], 32), (QWEN["gate_up"], 64),
-                           (QWEN["lm_head"], 5), (QWEN["lm_head"], 64), (QWEN["qkv"], 2)]:
-        assert lib.krk_gemm_normed_fused(M, N, K, epi, ctypes.byref(coop)) == 1, (N, M)
-    deep = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1, splits=1)
+        cfg = GemmConfig()
+        assert lib.krk_gemm_normed_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
+        assert cfg.prologue == 1 - fused, (N, M)
+        assert lib.krk_gemm_normed_fused(M, N, K, epi, ctypes.byref(cfg)) == fused, (N, M)
+    N, K, epi = QWEN["qkv"]
+    for kw, fused in [(dict(n_tiles=2, waves=8), 1), (dict(n_tiles=1, waves=4), 0), (dict(n_tiles=2, waves=8, splits=2), 0),
+                      (dict(n_tiles=2, waves=8, prologue=1), 0)]:
+        cfg = GemmConfig(kernel=_lib.KERNEL_VALU, unroll=5, **kw)
+        assert lib.krk_gemm_normed_fused(4, N, K, epi, ctypes.byref(cfg)) == fused, kw
+    for kernel in (_lib.KERNEL_STREAM, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_MFMA):
+        cfg = GemmConfig(kernel=kernel)
+        assert lib.krk_gemm_normed_fused(16, N, K, epi, ctypes.byref(cfg)) == 0
+    deep = GemmConfig(kernel=_lib.KERNEL_STREAM, splits=1)
     assert lib.krk_gemm_normed_fused(8, 2560, 9728, NONE, ctypes.byref(deep)) < 0  # 19 stages: not instantiated
     bad = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=2)
     assert lib.krk_gemm_normed_fused(8, 6144, 2560, NONE, ctypes.byref(bad)) == _lib.KRK_ERR_UNSUPPORTED
     assert lib.krk_gemm_normed_fused(0, 6144, 2560, NONE, None) == _lib.KRK_ERR_INVALID
-
-
-COOP_CTL_BYTES = 4 * (16 * 64 + 64 + 32 + 32)  # control block of the in-kernel prologue
+    assert lib.krk_gemm_normed_plan(1, 6144, 2560, NONE, None) == _lib.KRK_ERR_INVALID
 
 
 def test_normed_workspace_layouts(lib):
     """Prologue-kernel plans add the M normalised rows after the split-K area;
-    in-kernel-prologue (stream) plans add the control block and one copy of
-    the rows per die slot (16); fused VALU plans at M = 1 add nothing."""
-    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["qkv"], 4), (QWEN["qkv"], 100), (QWEN["gate_up"], 64),
-                           (QWEN["lm_head"], 17)]:
+    fused plans add nothing."""
+    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["qkv"], 100), (QWEN["gate_up"], 64), (QWEN["lm_head"], 64)]:
+        assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == 0
         plain = lib.krk_gemm_workspace_bytes(M, N, K, epi)
         normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None)
         assert normed == -(-plain // 256) * 256 + M * K * 2
-    coop = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1)
-    for (N, K, epi), M in [(QWEN["gate_up"], 64), (QWEN["lm_head"], 17), (QWEN["gate_up"], 100)]:
-        plain = lib.krk_gemm_config_workspace_bytes(M, N, K, epi, ctypes.byref(coop))
-        normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, ctypes.byref(coop))
-        tiles = -(-min(M, 64) // 16)  # the stream plan's 16-row tiles; the copies are in its fragment layout
-        assert normed == -(-plain // 256) * 256 + -(-COOP_CTL_BYTES // 256) * 256 + 16 * tiles * 16 * K * 2, (N, M)
-    for (N, K, epi), M in [(QWEN["qkv"], 1), (QWEN["gate_up"], 1)]:
-        assert lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None) == lib.krk_gemm_workspace_bytes(M, N, K, epi)
+    sep = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1)
+    for (N, K, epi), M in [(QWEN["gate_up"], 16), (QWEN["lm_head"], 17)]:
+        plain = lib.krk_gemm_config_workspace_bytes(M, N, K, epi, ctypes.byref(sep))
+        normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, ctypes.byref(sep))
+        assert normed == -(-plain // 256) * 256 + M * K * 2, (N, M)
+    for (N, K, epi), M in [(QWEN["qkv"], 1), (QWEN["gate_up"], 2), (QWEN["lm_head"], 1)]:
+        assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == 1
+        cfg = GemmConfig()
+        assert lib.krk_gemm_normed_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
+        assert lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None) == \
+            lib.krk_gemm_config_workspace_bytes(M, N, K, epi, ctypes.byref(cfg))
 
 
 @pytest.mark.parametrize("kw,code", [
