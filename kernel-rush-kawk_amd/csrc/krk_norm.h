@@ -75,8 +75,7 @@ __device__ __forceinline__ u32x4 normalize_bf16x8(const u32x4& s, float rstd, co
 }
 
 // Two fp32 values -> packed bf16 bits (lo in bits 0-15), round to nearest
-// even by gfx950's v_cvt_pk_bf16_f32 (the same bits as f32_to_bf16 for every
-// non-NaN input; a NaN stays a NaN).
+// even by gfx950's v_cvt_pk_bf16_f32 (each half the bits f32_to_bf16 gives).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 v;
     v[0] = (__bf16)lo;
