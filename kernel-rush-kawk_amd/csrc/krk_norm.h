@@ -100,26 +100,6 @@ __device__ __forceinline__ u32x4 add_sumsq_bf16x8(const u32x4& x, const u32x4& d
     return s;
 }
 
-// n = bf16(bf16(s · rstd) · wn) for 8 elements (hardware conversions).
-__device__ __forceinline__ u32x4 normalize_hw_bf16x8(const u32x4& s, float rstd, const u32x4& wn) {
-    u32x4 r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t nj = pack_bf16x2(bf16_to_f32(s[j] & 0xffffu) * rstd, bf16_to_f32(s[j] >> 16) * rstd);
-        r[j] = pack_bf16x2(bf16_to_f32(nj & 0xffffu) * bf16_to_f32(wn[j] & 0xffffu),
-                           bf16_to_f32(nj >> 16) * bf16_to_f32(wn[j] >> 16));
-    }
-    return r;
-}
-
-// Σ over the wave of a per-lane value, the same in every lane: a fixed xor
-// butterfly, then lane 0's sum broadcast.
-__device__ __forceinline__ float wave_sum_uniform(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
-
 __device__ __forceinline__ float rms_rstd(float sumsq, int K, float eps) {
     return __frsqrt_rn(sumsq / (float)K + eps);
 }
@@ -154,9 +134,9 @@ add_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t ldx, NormArgs a,
             ss = sumsq_bf16x8(s[v], ss);
         }
     }
-    // Fixed-order reduction: xor butterfly within the wave, then waves in order.
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    // Fixed-order reduction: butterfly within the wave (every lane ends with
+    // the same sum), then waves in order.
+    wave_fold<1, 32>(&ss, lane);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     float tot = red[0];

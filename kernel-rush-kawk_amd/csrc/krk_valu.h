@@ -61,71 +61,6 @@ __device__ __forceinline__ u32x4 load_row16(const uint16_t* base, uint32_t byte_
     return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_move(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-// Partner of a lane in the butterfly step on bit STEP.  Across rows (32, 16)
-// the gfx950 permlane swaps exchange whole rows; within a row DPP row_mirror
-// (lane i <-> 15 - i), row_half_mirror (i <-> 7 - i) and quad_perm (i ^ 2,
-// i ^ 1).  Each partner differs from the lane in bit STEP.
-template <int STEP>
-__device__ __forceinline__ float partner(float v) {
-    if constexpr (STEP == 8) return dpp_move<0x140>(v);
-    if constexpr (STEP == 4) return dpp_move<0x141>(v);
-    if constexpr (STEP == 2) return dpp_move<0x4E>(v);
-    if constexpr (STEP == 1) return dpp_move<0xB1>(v);
-    return v;
-}
-
-// Sum of a lane's pair (lo, hi) with its partner's on the bit-STEP step:
-// lanes with the bit clear get lo + partner's lo, the others hi + partner's hi.
-template <int STEP>
-__device__ __forceinline__ float fold_pair(float lo, float hi, int lane) {
-    if constexpr (STEP == 32 || STEP == 16) {
-        // permlane swap (vdst = lo, src = hi): with the bit clear vdst keeps
-        // the lane's lo and src receives the partner's lo; with it set vdst
-        // receives the partner's hi and src keeps the lane's hi.
-        const auto r = STEP == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false)
-                                  : __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    } else {
-        const bool up = (lane & STEP) != 0;
-        const float give = up ? lo : hi;
-        const float keep = up ? hi : lo;
-        return keep + partner<STEP>(give);
-    }
-}
-
-// Fold N values per lane across the wave.  While N > 1 each step keeps half of
-// the values (the lane's bit STEP picks which half) and adds the partner's
-// copy of that half; once N == 1 each step adds the partner's value.
-// Afterwards lane l holds the wave sum of value (l >> (6 - p)) & (N0 - 1),
-// N0 = 2^p the starting count.
-template <int N, int STEP>
-__device__ __forceinline__ void wave_fold(float* v, int lane) {
-    if constexpr (STEP >= 1) {
-        if constexpr (N > 1) {
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) v[i] = fold_pair<STEP>(v[i], v[i + N / 2], lane);
-            wave_fold<N / 2, STEP / 2>(v, lane);
-        } else {
-            v[0] = fold_pair<STEP>(v[0], v[0], lane);
-            wave_fold<1, STEP / 2>(v, lane);
-        }
-    }
-}
-
-template <int V>
-constexpr int log2_exact() {
-    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "power of two up to 64");
-    if constexpr (V == 1) {
-        return 0;
-    } else {
-        return 1 + log2_exact<V / 2>();
-    }
-}
-
 // MX: x rows held (>= M); R: W rows per wave (for SILU R/2 gate rows then the
 // matching R/2 up rows); D: 512-element blocks loaded per row before the wave
 // consumes them; EXACT: K is whole blocks and every split is whole chunks of D
@@ -331,7 +266,7 @@ __global__ __launch_bounds__(64 * kValuMaxWaves) void valu_gemm_kernel(
                 for (int wv = 1; wv < waves; ++wv) t += red[wv * MX + m];
                 const float rstd = rms_rstd(t, K, na.eps);
                 *reinterpret_cast<u32x4*>(xs + ((size_t)(m * nb + bw) * kValuBlock + lane_k) * 2) =
-                    normalize_hw_bf16x8(xr[m], rstd, gv);
+                    normalize_bf16x8(xr[m], rstd, gv);
             }
         }
         lds_wait();
