@@ -124,7 +124,9 @@ typedef struct krk_gemm_config {
                      1 = always the separate prologue kernel.  Ignored by
                      plain calls. */
     int channels; /* MFMA_LDS: output channels per workgroup, a multiple of 8 up
-                     to 16·n_tiles (8·n_tiles with SILU_MUL); 0 = all of them.
+                     to 16·n_tiles (8·n_tiles with SILU_MUL); 0 = the
+                     dispatcher's choice (the plan's when the plan uses this
+                     kernel and tile width, else all of them).
                      Fewer channels than the tiles hold leave the rest of the
                      last tile as padding (not loaded), so a shape can be cut
                      into exactly as many blocks as there are CUs.  Other
