@@ -291,6 +291,41 @@ SPECIAL_FAMILIES = [
 ]
 
 
+# (a, b) pairs whose fp32 sum a + b is exact and lies exactly halfway between
+# two bf16 values (or just above it): the epilogue's round-to-nearest-even
+# decides the output bits.
+TIE_PAIRS = [(1.0, 2.0 ** -8), (1.0 + 2.0 ** -7, 2.0 ** -8), (1.0, 2.0 ** -8 + 2.0 ** -15), (256.0, 1.0),
+             (258.0, 1.0), (-1.0, -(2.0 ** -8)), (-(1.0 + 2.0 ** -7), -(2.0 ** -8)), (3.0, 2.0 ** -7),
+             (2.0 ** -120, 2.0 ** -128), (65280.0, 128.0)]
+
+
+@pytest.mark.parametrize("family,M,config", SPECIAL_FAMILIES, ids=[f[0] for f in SPECIAL_FAMILIES])
+def test_round_half_even_outputs(device, family, M, config):
+    """Each row of x holds two ones (in different halves of K, so different
+    splits and stages); each W channel holds a tie pair (a, b) at those two
+    columns.  y = bf16(a + b) with the sum exact in fp32, so the output bits
+    are fixed by round-to-nearest-even alone, in every kernel family."""
+    K, N = 2560, 96
+    w = R.randn_bf16((N, K), 7950, 0.02)
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    a = torch.tensor([TIE_PAIRS[n % len(TIE_PAIRS)][0] for n in range(N)], dtype=torch.bfloat16)
+    b = torch.tensor([TIE_PAIRS[n % len(TIE_PAIRS)][1] for n in range(N)], dtype=torch.bfloat16)
+    assert torch.equal(a.float(), torch.tensor([p[0] for p in TIE_PAIRS] * 10)[:N]) and \
+        torch.equal(b.float(), torch.tensor([p[1] for p in TIE_PAIRS] * 10)[:N]), "tie pairs must be bf16 values"
+    for m in range(M):
+        k1 = (37 + 71 * m) % (K // 2)
+        k2 = K // 2 + (5 + 53 * m) % (K // 2)
+        x[m, k1] = 1.0
+        x[m, k2] = 1.0
+        w[:, k1] = a
+        w[:, k2] = b
+    expected = (a.float() + b.float()).to(torch.bfloat16).expand(M, N)
+    say("round half even", family, M, config)
+    y = krk(x, w, NONE, config)
+    assert torch.equal(y.view(torch.int16), expected.view(torch.int16)), \
+        f"{family}: {(y != expected).sum().item()} outputs off the round-to-nearest-even bits"
+
+
 def _special_operands(M, N, K, seed):
     """Random operands with NaN, +-inf and -0 planted in x rows and W rows.
     x: row 0 NaN at one k; row 1 +inf; row 2 -inf and +inf (products of
