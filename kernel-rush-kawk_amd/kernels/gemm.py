@@ -563,8 +563,9 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
     ``kind`` is "matmul" or "gateup".  Tuned like :func:`pick_matmul` over
     whole normed calls (the prologue fused or as its own kernel, as each
     configuration runs it), then validated once against the torch
-    composition (xout bit-exact, projection within the reference's
-    ``0.02·max|ref| + 1e-3``); with ``log`` the graph-replay time is logged."""
+    composition (xout bit-exact, projection under :func:`_validate`'s rule);
+    with ``log`` the graph-replay time is logged.  Without tuning the
+    library's normed plan runs."""
     if kind not in ("matmul", "gateup"):
         raise ValueError(f"kind must be 'matmul' or 'gateup', got {kind!r}")
     M, K = x.shape
