@@ -443,6 +443,26 @@ def _projection(M: int, N: int, K: int, epilogue: int, device, config: dict | No
     return SkinnyMatmul(M, N, K, device, config=config)
 
 
+def _validation_plan(M: int, epilogue: int, w, rot: list):
+    """Weights a tuning candidate is validated on, and whether the
+    reference's pointwise M = 64 gate/up rule applies as well.  Every
+    candidate runs on the call's weight and a second one of the rotation; a
+    gate/up projection of 64 or more rows runs on every distinct weight of the
+    rotation and must also meet ``0.02·|ref| + 1e-3`` at every element, as
+    the reference's M = 64 gate/up picker requires across its 36 layer
+    weights (engine/kernels/m64_gateup_selection.py:71-97)."""
+    strict = epilogue == EPILOGUE_SILU_MUL and M >= 64
+    if strict:
+        checks, seen = [], set()
+        for v in [w] + list(rot):
+            if id(v) not in seen:
+                seen.add(id(v))
+                checks.append(v)
+    else:
+        checks = [w] + [v for v in rot[1:2] if v is not w]
+    return checks, strict
+
+
 def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_NONE, ws: list | None = None,
                     log=None, cache=None, norm=None, limit: int | None = None):
     """Tune the projection ``a @ w.T`` (with ``epilogue``, and with the
@@ -457,9 +477,15 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
     rot = ws or [w]
     cache = tune.default_cache() if cache is None else cache
     kind = "gateup" if epilogue == EPILOGUE_SILU_MUL else "matmul"
-    # Candidates are validated on the call's weight and on a second one of
-    # the rotation, each against its own fp32-accumulated torch result.
-    checks = [w] + [v for v in rot[1:2] if v is not w]
+    # Candidates are validated against each weight's own fp32-accumulated
+    # torch result (which weights, and which rules: _validation_plan).
+    checks, strict = _validation_plan(M, epilogue, w, rot)
+
+    def judge(out, ref):
+        ok, why = tune.close_ok(out, ref)
+        if ok and strict:
+            ok, why = tune.pointwise_ok(out, ref)
+        return ok, why
 
     def project(inp, weight):
         ref = _linear_fp32acc(inp, weight)
@@ -474,7 +500,7 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
 
         def accept(fn):
             for v, ref in zip(checks, refs):
-                ok, why = tune.close_ok(fn(v), ref)
+                ok, why = judge(fn(v), ref)
                 if not ok:
                     return ok, why
             return ok, why
@@ -495,7 +521,7 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
                 out = fn(v)
                 if not torch.equal(xout, ref_xout):
                     return False, "xout differs from x + y"
-                ok, why = tune.close_ok(out, ref)
+                ok, why = judge(out, ref)
                 if not ok:
                     return ok, why
             return ok, why

@@ -158,6 +158,23 @@ def close_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
     return True, f"max err {worst:.4g}"
 
 
+def pointwise_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
+    """The reference's acceptance of its M = 64 gate/up kernels
+    (engine/kernels/m64_gateup_selection.py:71-97): both outputs finite and
+    ``|out - ref| <= 0.02 * |ref| + 1e-3`` at every element (tighter than
+    :func:`close_ok`'s elementwise bar wherever ``|ref| < ~1.9``)."""
+    out, ref = out.float(), ref.float()
+    if out.shape != ref.shape:
+        return False, f"shape {tuple(out.shape)} vs {tuple(ref.shape)}"
+    if not (torch.isfinite(out).all() and torch.isfinite(ref).all()):
+        return False, "non-finite output or reference"
+    err = (out - ref).abs()
+    bad = int((err > 0.02 * ref.abs() + 1e-3).sum())
+    if bad:
+        return False, f"{bad} elements outside 0.02*|ref| + 1e-3 (max err {err.max().item():.4g})"
+    return True, f"max err {err.max().item():.4g}"
+
+
 def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, accept, timer, rot: list,
            log=None, cache: TuneCache | None = None, limit: int | None = None,
            extra: list | None = None, plan: dict | None = None) -> Result:

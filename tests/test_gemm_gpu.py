@@ -729,16 +729,18 @@ _TUNE_SHAPES = {"qkv": (2560, 6144, NONE), "o": (4096, 2560, NONE), "gate_up": (
                 "down": (9728, 2560, NONE), "lm_head": (2560, 151936, NONE)}
 
 
-@pytest.mark.parametrize("shape,M", [("qkv", 8), ("gate_up", 4), ("down", 32), ("o", 64), ("lm_head", 1)])
+@pytest.mark.parametrize("shape,M", [("qkv", 8), ("gate_up", 4), ("down", 32), ("o", 64), ("lm_head", 1),
+                                     ("gate_up", 64)])
 def test_tune_validates_every_candidate(device, shape, M):
     """The tuner runs every candidate configuration at a real shape: each
-    must pass the reference's acceptance rule (a rejection is a kernel bug),
-    the winner is no slower than the table's plan, and a second tuning of
-    the shape comes from the cache."""
+    must pass the acceptance rules (a rejection is a kernel bug; gate_up at
+    M = 64 also meets the reference's pointwise M = 64 rule on every weight
+    of a 6-weight rotation), the winner is no slower than the table's plan,
+    and a second tuning of the shape comes from the cache."""
     from kernels import tune as T
     K, N, epi = _TUNE_SHAPES[shape]
     a = R.randn_bf16((M, K), 9600 + M).to(device)
-    ws = [R.randn_bf16((N, K), 9601 + i, 0.02).to(device) for i in range(2)]
+    ws = [R.randn_bf16((N, K), 9601 + i, 0.02).to(device) for i in range(6 if (shape, M) == ("gate_up", 64) else 2)]
     cache = T.TuneCache()
     say("tune", shape, M, len(T.candidates(M, N, K, epi)), "candidates")
     r = G.tune_projection(a, ws[0], epi, ws=ws, cache=cache)

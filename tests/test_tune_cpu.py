@@ -218,3 +218,40 @@ def test_acceptance_rule_is_elementwise():
     assert not close_ok(out, inf_ref)[0]
     out[0, 0] = float("inf")
     assert close_ok(out, inf_ref)[0]
+
+
+def test_pointwise_rule_of_the_m64_gateup_picker():
+    """pointwise_ok: |out - ref| <= 0.02|ref| + 1e-3 at every element and
+    everything finite (the reference's M = 64 gate/up acceptance).  An error
+    the elementwise bar accepts near a small reference value fails it."""
+    import torch
+    from kernels.tune import close_ok, pointwise_ok
+
+    ref = torch.linspace(-3, 3, 401)
+    assert pointwise_ok(ref.clone(), ref)[0]
+    out = ref.clone()
+    out[200] += 5e-3                      # ref[200] = 0: allowed 1e-3 here, 2e-2 by close_ok
+    assert close_ok(out, ref)[0] and not pointwise_ok(out, ref)[0]
+    out = ref * (1 + 0.019)               # within 2% everywhere
+    assert pointwise_ok(out, ref)[0]
+    bad = ref.clone()
+    bad[5] = float("inf")
+    assert not pointwise_ok(bad, ref)[0]
+    assert not pointwise_ok(ref[:10], ref)[0]
+
+
+def test_validation_plan_of_the_tuner():
+    """Candidates run on the call's weight and a second rotation weight; a
+    gate/up projection of 64 rows or more runs on every distinct weight of
+    the rotation under the pointwise rule as well."""
+    from kernels.gemm import EPILOGUE_NONE, EPILOGUE_SILU_MUL, _validation_plan
+
+    w, rot = object(), [object() for _ in range(5)]
+    checks, strict = _validation_plan(32, EPILOGUE_SILU_MUL, w, [w] + rot)
+    assert checks == [w, rot[0]] and not strict
+    checks, strict = _validation_plan(64, EPILOGUE_NONE, rot[2], rot)
+    assert checks == [rot[2], rot[1]] and not strict
+    checks, strict = _validation_plan(64, EPILOGUE_SILU_MUL, w, [w] + rot + [rot[0]])
+    assert checks == [w] + rot and strict
+    checks, strict = _validation_plan(64, EPILOGUE_SILU_MUL, w, [w])
+    assert checks == [w] and strict
