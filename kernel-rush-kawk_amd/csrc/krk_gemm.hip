@@ -167,11 +167,11 @@ const TableEntry kTable[] = {
     {2560, 1216, KRK_EPILOGUE_NONE, 25, 48, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 256)},
     {2560, 1216, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
     // lm_head shard 2560 -> 18992
-    {18992, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    {18992, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
     {18992, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {18992, 2560, KRK_EPILOGUE_NONE, 3, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {18992, 2560, KRK_EPILOGUE_NONE, 9, 24, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
-    {18992, 2560, KRK_EPILOGUE_NONE, 25, 48, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    {18992, 2560, KRK_EPILOGUE_NONE, 25, 48, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
     {18992, 2560, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_STREAM, 1, 3, 0, 1)},
 };
 
