@@ -114,7 +114,7 @@ typedef struct krk_gemm_config {
                      loads in flight per lane); MFMA_LDS: stages in flight (2, or 3
                      when m_tiles + n_tiles <= 6); STREAM: ring depth in 512-k
                      stages (2..8, less at large M) */
-    int waves;    /* waves per workgroup (MFMA: 1, 2, 4; VALU: 1, 2, 4, 8; MFMA_LDS and STREAM: 8) */
+    int waves;    /* waves per workgroup (MFMA: 1, 2, 4; VALU: 1 to 8; MFMA_LDS and STREAM: 8) */
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
     int k_chunk;  /* MFMA_LDS: k per pipeline stage, 256 or 512 (512 needs
                      m_tiles + n_tiles <= 4); other kernels: ignored */

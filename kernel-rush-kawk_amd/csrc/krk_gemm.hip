@@ -109,9 +109,11 @@ const TableEntry kTable[] = {
     {6144, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1, 512, 24)},
     {6144, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256, 24)},
     // o_proj 4096 -> 2560
-    {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 3, 8, kcfg(KRK_KERNEL_VALU, 2, 4, 8, 1)},
+    // 5-wave workgroups: 256 of 2 rows per wave at M <= 2, 512 of 1 at M = 3-6
+    {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 4, 5, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 8, 5, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 3, 6, kcfg(KRK_KERNEL_VALU, 1, 4, 5, 1)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 7, 8, kcfg(KRK_KERNEL_VALU, 2, 4, 8, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
     {2560, 4096, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 4096, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3)},
@@ -122,7 +124,7 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
-    {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 2, 1)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 5, 1)},
     {2560, 9728, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 2, 8, 3)},
     {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
     {2560, 9728, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
@@ -404,8 +406,8 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
             return fail(KRK_ERR_UNSUPPORTED, "VALU n_tiles (W rows per wave)=%d not in {1,2,4}", c.n_tiles);
         if (silu && c.n_tiles % 2)
             return fail(KRK_ERR_UNSUPPORTED, "SILU_MUL needs an even n_tiles (gate and up rows), got %d", c.n_tiles);
-        if (c.waves != 1 && c.waves != 2 && c.waves != 4 && c.waves != krk::kValuMaxWaves)
-            return fail(KRK_ERR_UNSUPPORTED, "VALU waves=%d not in {1,2,4,%d}", c.waves, krk::kValuMaxWaves);
+        if (c.waves < 1 || c.waves > krk::kValuMaxWaves)
+            return fail(KRK_ERR_UNSUPPORTED, "VALU waves=%d not in 1..%d", c.waves, krk::kValuMaxWaves);
         const int nb = cdiv(K, krk::kValuBlock);
         if (c.splits < 1 || c.splits > 32 || c.splits > nb)
             return fail(KRK_ERR_UNSUPPORTED, "VALU splits=%d not in 1..min(32, %d K blocks)", c.splits, nb);
@@ -776,7 +778,8 @@ bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
 // measured fastest (tuner, graph replay over rotating weights, MI355X); every
 // other shape and M runs its plain plan behind the prologue kernel.
 const TableEntry kNormTable[] = {
-    {6144, 2560, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_VALU, 4, 5, 8, 1)},
+    // qkv: 256 workgroups of 6 waves x 4 rows
+    {6144, 2560, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_VALU, 4, 5, 6, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 5, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
@@ -1426,10 +1429,12 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
     const int nts[] = {1, 2, 4};
     const int splits[] = {1, 2, 3, 4};
     // VALU: unroll 0 covers a split's K range in one pass; 2 and 4 blocks in
-    // flight per row leave more waves resident (fewer VGPRs).
+    // flight per row leave more waves resident (fewer VGPRs).  5 and 6 waves
+    // cut some grids to exactly one workgroup per CU (o: 2560 channels = 256
+    // workgroups of 5 waves x 2 rows; qkv: 6144 = 256 x 6 waves x 4 rows).
     if (Mc <= kValuMaxRows)
         for (int nt : nts)
-            for (int wv : {4, krk::kValuMaxWaves})
+            for (int wv : {4, 5, 6, krk::kValuMaxWaves})
                 for (int sp : splits)
                     for (int u : {0, 2, 4}) add(krk_gemm_config{KRK_KERNEL_VALU, 0, nt, u, wv, sp, 0});
     // More splits for the weight-streaming MFMA kernels: at M >= 16 they cut

@@ -171,6 +171,7 @@ def test_config_errors(lib, cfg, code, msg):
     (dict(kernel=2, unroll=6), "unroll"),
     (dict(kernel=2, n_tiles=4, unroll=19), "unroll"),
     (dict(kernel=2, waves=16), "waves"),
+    (dict(kernel=2, waves=9), "waves"),
     (dict(kernel=2, splits=6), "splits"),
 ])
 def test_valu_config_errors(lib, cfg, msg):
@@ -282,7 +283,8 @@ def test_normed_fused_plans(lib):
         assert cfg.prologue == 1 - fused, (N, M)
         assert lib.krk_gemm_normed_fused(M, N, K, epi, ctypes.byref(cfg)) == fused, (N, M)
     N, K, epi = QWEN["qkv"]
-    for kw, fused in [(dict(n_tiles=2, waves=8), 1), (dict(n_tiles=1, waves=4), 0), (dict(n_tiles=2, waves=8, splits=2), 0),
+    for kw, fused in [(dict(n_tiles=2, waves=8), 1), (dict(n_tiles=1, waves=4), 0), (dict(n_tiles=1, waves=5), 1),
+                      (dict(n_tiles=4, waves=6), 1), (dict(n_tiles=2, waves=8, splits=2), 0),
                       (dict(n_tiles=2, waves=8, prologue=1), 0)]:
         cfg = GemmConfig(kernel=_lib.KERNEL_VALU, unroll=5, **kw)
         assert lib.krk_gemm_normed_fused(4, N, K, epi, ctypes.byref(cfg)) == fused, kw

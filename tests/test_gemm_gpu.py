@@ -458,7 +458,7 @@ def _stream_configs(M, K):
 
 
 def _valu_configs(silu, depths=(2, 3, 5, 7, 19)):
-    for wv, nt, d, sp in itertools.product((1, 8), (1, 2, 4), depths, (1, 3)):
+    for wv, nt, d, sp in itertools.product((1, 5, 8), (1, 2, 4), depths, (1, 3)):
         if silu and nt % 2:
             continue
         yield dict(kernel=_lib.KERNEL_VALU, waves=wv, n_tiles=nt, unroll=d, splits=sp)
@@ -570,13 +570,19 @@ def test_valu_gateup_configs(device, M, I, K):
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_valu_qwen_shapes(device, M):
     """The VALU kernel on the real projection shapes, including down's 19
-    K blocks (several passes of the block loop) and the widest split."""
+    K blocks (several passes of the block loop), the widest split and
+    workgroups of 3, 5 and 6 waves (grids whose last workgroup is partly
+    past N: o's 2560 channels over 3 x 1 per workgroup, qkv's 6144 over
+    5 x 2)."""
     for name, (N, K, epi) in {"qkv": (6144, 2560, NONE), "o": (2560, 4096, NONE), "down": (2560, 9728, NONE),
                               "gate_up": (19456, 2560, SILU)}.items():
         x = R.randn_bf16((M, K), 9300 + M + K)
         w = R.randn_bf16((N, K), 9301 + N, 0.02)
         cfgs = [dict(kernel=_lib.KERNEL_VALU, n_tiles=2, waves=8, unroll=5, splits=1),
-                dict(kernel=_lib.KERNEL_VALU, n_tiles=4, waves=4, unroll=4, splits=2)]
+                dict(kernel=_lib.KERNEL_VALU, n_tiles=4, waves=4, unroll=4, splits=2),
+                dict(kernel=_lib.KERNEL_VALU, n_tiles=2, waves=5, unroll=4, splits=1),
+                dict(kernel=_lib.KERNEL_VALU, n_tiles=4, waves=6, unroll=5, splits=1),
+                dict(kernel=_lib.KERNEL_VALU, n_tiles=1, waves=3, unroll=2, splits=3)]
         if name == "down":
             cfgs.append(dict(kernel=_lib.KERNEL_VALU, n_tiles=1, waves=8, unroll=10, splits=1))
             cfgs.append(dict(kernel=_lib.KERNEL_VALU, n_tiles=2, waves=8, unroll=3, splits=4))
