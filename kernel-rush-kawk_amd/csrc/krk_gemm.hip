@@ -516,12 +516,13 @@ int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false>
-int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::SelectArgs sa = {}) {
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false>
+int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::SelectArgs sa = {},
+                    krk::NormArgs na = {}) {
     if constexpr ((PF == 3 && !mfma_lds_pf3(MT, NT)) || !krk::mfma_lds_kc_ok(MT, NT, KC)) {
         return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS unroll=%d k_chunk=%d with %d x %d tiles", PF, KC, MT, NT);
     } else {
-        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU, SEL>);
+        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU, SEL, NORM>);
         const size_t shm = krk::mfma_lds_bytes(MT, NT, KC, SEL);
         // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once
         // per instantiation (a function attribute, not a stream operation).
@@ -531,7 +532,7 @@ int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::S
         int cb = a.cb;
         void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
                         (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&cb, (void*)&a.part,
-                        (void*)&a.ctr, (void*)&sa};
+                        (void*)&a.ctr, (void*)&sa, (void*)&na};
         hipError_t e = hipLaunchKernel(fn, dim3(nblocks * a.splits), dim3(64 * krk::kLdsWaves), args, shm, stream);
         return hip_status(e, "mfma_lds_kernel launch");
     }
@@ -751,11 +752,38 @@ int dispatch_valu_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblock
     return fail(KRK_ERR_UNSUPPORTED, "VALU normed: x rows=%d", c.m_tiles);
 }
 
+// The LDS-staged kernel with the fused prologue: 512-k stages, K unsplit, one
+// 16-row x tile (the normalised rows of all stages stay in registers: with
+// two tiles the kernel spills), one or two weight tiles.
+constexpr int kLdsNormMaxMTiles = 1;
+constexpr int kLdsNormMaxNTiles = 2;
+
+template <int MT, int NT, bool SILU>
+int dispatch_mfma_lds_norm_pf(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                              const krk::NormArgs& na) {
+    if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, true>(a, nblocks, s, {}, na);
+    return launch_mfma_lds<MT, NT, 2, 512, SILU, false, true>(a, nblocks, s, {}, na);
+}
+
+template <bool SILU>
+int dispatch_mfma_lds_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
+                           const krk::NormArgs& na) {
+    if constexpr (!SILU) {
+        if (c.m_tiles == 1 && c.n_tiles == 1) return dispatch_mfma_lds_norm_pf<1, 1, false>(a, c, nblocks, s, na);
+    }
+    if (c.m_tiles == 1 && c.n_tiles == 2) return dispatch_mfma_lds_norm_pf<1, 2, SILU>(a, c, nblocks, s, na);
+    return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS normed: m_tiles=%d n_tiles=%d", c.m_tiles, c.n_tiles);
+}
+
 // Whether a resolved configuration fuses the RMSNorm prologue into the
 // projection kernel (one launch), else a separate prologue kernel writes the
 // normalised rows first (also what prologue = 1 asks for).  Both keep the
-// reference's rounding points (krk_norm.h).  Fused: a VALU configuration,
-// K unsplit, at the depth covering K = 2560, with a wave per 512-k block.
+// reference's rounding points (krk_norm.h).  Fused, with K unsplit:
+//   * a VALU configuration at the depth covering K = 2560, with a wave per
+//     512-k block (M <= 8);
+//   * an LDS-staged MFMA configuration with 512-k stages, K <= 2560, one x
+//     tile and one or two weight tiles (M <= 16; the reference offers its
+//     fused prologue up to M = 32, engine/kernels/gemm.py:524-531).
 //
 // Every workgroup of a fused call normalises all M rows itself (about ten
 // VALU instructions per element), so the fused form pays only at small M:
@@ -769,8 +797,12 @@ bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
     (void)M;
     (void)N;
     (void)epilogue;
-    if (c.prologue != 0 || c.splits != 1 || c.kernel != KRK_KERNEL_VALU) return false;
+    if (c.prologue != 0 || c.splits != 1) return false;
     const int nb = cdiv(K, krk::kValuBlock);
+    if (c.kernel == KRK_KERNEL_MFMA_LDS)
+        return c.k_chunk == 512 && nb <= krk::kLdsNormStages && c.m_tiles <= kLdsNormMaxMTiles &&
+               c.n_tiles <= kLdsNormMaxNTiles;
+    if (c.kernel != KRK_KERNEL_VALU) return false;
     return c.unroll == kValuNormDepth && nb <= c.waves && krk::valu_norm_lds_bytes(c.m_tiles, nb) <= kLdsMax;
 }
 
@@ -778,8 +810,11 @@ bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
 // measured fastest (tuner, graph replay over rotating weights, MI355X); every
 // other shape and M runs its plain plan behind the prologue kernel.
 const TableEntry kNormTable[] = {
-    // qkv: 256 workgroups of 6 waves x 4 rows
+    // qkv: 256 workgroups of 6 waves x 4 rows; at M = 5-16 the LDS-staged
+    // kernel's fused form on 192 blocks of 32 channels (7-12% under the
+    // prologue kernel + plain plan)
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_VALU, 4, 5, 6, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 5, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
@@ -939,7 +974,12 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
             krk::NormArgs nc = na;
             nc.d += (int64_t)m0 * na.ldd;
             nc.xout += (int64_t)m0 * na.ldxo;
-            rc = silu ? dispatch_valu_norm<true>(a, c, g.nblocks, st, nc) : dispatch_valu_norm<false>(a, c, g.nblocks, st, nc);
+            if (c.kernel == KRK_KERNEL_MFMA_LDS)
+                rc = silu ? dispatch_mfma_lds_norm<true>(a, c, g.nblocks, st, nc)
+                          : dispatch_mfma_lds_norm<false>(a, c, g.nblocks, st, nc);
+            else
+                rc = silu ? dispatch_valu_norm<true>(a, c, g.nblocks, st, nc)
+                          : dispatch_valu_norm<false>(a, c, g.nblocks, st, nc);
         } else if (c.kernel == KRK_KERNEL_MFMA) {
             rc = silu ? dispatch_mfma<true>(a, c, g.nblocks, st) : dispatch_mfma<false>(a, c, g.nblocks, st);
         } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {

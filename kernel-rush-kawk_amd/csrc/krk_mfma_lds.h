@@ -36,11 +36,15 @@
 #pragma once
 
 #include "krk_epilogue.h"
+#include "krk_norm.h"
 #include "krk_select.h"
 
 namespace krk {
 
 constexpr int kLdsWaves = 8;
+// Stages of 512 k the fused RMSNorm prologue holds in registers: K <= 2560,
+// the hidden size every normed projection reads.
+constexpr int kLdsNormStages = 5;
 
 // k per stage: 512 fits two tiles of NR + MX rows in LDS up to four 16-row
 // tiles (128 KB); 256 halves the footprint (more workgroups per CU when the
@@ -58,19 +62,29 @@ __host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool
 
 // SEL: per-workgroup argmax keys for token selection (krk_select.h) instead
 // of, or besides, storing y (y may be null); K unsplit.
+// NORM: x is the residual stream and the projection input is
+// rms_norm(x + na.d) with the rounding points of krk_norm.h, K unsplit in
+// 512-k stages, at most kLdsNormStages of them.  Wave w owns x rows w, w + 8,
+// ... (the rows it stages anyway): before the first stage it loads x, d and
+// the gain for every stage of its rows, then the first weight stages, then
+// forms s = bf16(x + d), takes each row's Σ s² with a wave butterfly and
+// keeps the normalised rows in registers, from which every stage's x rows
+// are staged; no x loads remain in the loop.  Workgroup 0 writes s to
+// na.xout after the loop.
 // cb: output channels per block (a multiple of 8, at most 16·NH).  Below
 // 16·NH the last tile is partly padding: its rows past cb are not loaded
 // (zeros in the tile) and their outputs not stored.  This lets a shape use
 // all 256 CUs with whole K (qkv: 6144 = 256 x 24 channels) instead of
 // leaving CUs idle or splitting K.
-template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false>
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false>
 __global__ void __launch_bounds__(64 * kLdsWaves)
 mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const uint16_t* __restrict__ w, int64_t ldw,
                 uint16_t* __restrict__ y, int64_t ldy,
                 int M, int N, int K, int splits, int cb,
-                float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa) {
+                float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa, NormArgs na) {
     static_assert(!(SEL && SILU), "selection reads plain logits");
+    static_assert(!NORM || (KC == 512 && !SEL), "the fused prologue stages whole 512-k x rows");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     static_assert(!SILU || (NT % 2 == 0), "SILU pairs gate and up tiles");
     static_assert(PF >= 2, "at least two stages in flight");
@@ -131,16 +145,29 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         for (int t = 0; t < NT; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Stage st into registers.  Prefetches past the range read the start of
-    // x row 0 instead (valid, L2-resident, never used), so every step issues
-    // the same loads and the compiler's waits stay exact.
+    // x row 0 instead (valid, L2-resident, never used).  The padding rows
+    // past the block's cb channels are not loaded in the plain kernel; the
+    // compiler then counts only the unconditional loads in its waits, which
+    // wait for the next stage's weight loads too (measured: loading the
+    // padding rows from x instead, so that the waits keep a whole stage in
+    // flight, made qkv and down at M = 64 3-6% slower).  With NORM every
+    // load is unconditional: there the waits in the prologue must not drain
+    // the first weight stages.
     auto load = [&](u32x4 (&R)[LPW], int st, bool live) {
         const int kk = st * KC + 8 * lsub < K ? st * KC : -8 * lsub;  // past K: the row's start
         const int xo = 8 * lsub < K ? 8 * lsub : K - 8;
 #pragma unroll
-        for (int j = 0; j < LW; ++j)
-            R[j] = rowok[j] ? load_stream16(live ? rowp[j] + kk : x + xo) : u32x4{0u, 0u, 0u, 0u};
+        for (int j = 0; j < LW; ++j) {
+            if constexpr (NORM) {
+                R[j] = load_stream16(live && rowok[j] ? rowp[j] + kk : x + xo);
+            } else {
+                R[j] = rowok[j] ? load_stream16(live ? rowp[j] + kk : x + xo) : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+        if constexpr (!NORM) {
 #pragma unroll
-        for (int j = 0; j < LX; ++j) R[LW + j] = load_cached16(live ? rowp[LW + j] + kk : x + xo);
+            for (int j = 0; j < LX; ++j) R[LW + j] = load_cached16(live ? rowp[LW + j] + kk : x + xo);
+        }
     };
     auto stash = [&](const u32x4 (&R)[LPW], int st, unsigned char* tile) {
         const bool rag = ragged_k && st == KST - 1;
@@ -149,6 +176,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         for (int j = 0; j < LPW; ++j) {
             const int tr = j < LW ? RPL * (wave + WV * j) + lrow : NR + RPL * (wave + WV * (j - LW)) + lrow;
             u32x4 v = R[j];
+            if (NORM && j < LW && !rowok[j]) v = u32x4{0u, 0u, 0u, 0u};  // padding row (placeholder load)
             if (rag) v &= mk;
             *reinterpret_cast<u32x4*>(tile + tr * PITCH + 16 * (lsub ^ (tr & 15))) = v;
         }
@@ -174,7 +202,92 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         }
     };
 
-    if (sb < se) {
+    if constexpr (NORM) {
+        // K unsplit (sb = 0) in nst <= XN stages of 512: lane l of wave w
+        // holds k = 512·b + 8l of rows w + 8j for every stage b.  Rows past
+        // M and k past K are zero.
+        constexpr int XN = kLdsNormStages;
+        const int nst = KST;
+        u32x4 xr[XN][LX], dr[XN][LX], gv[XN];
+        u32x4 sv[XN][LX];
+#pragma unroll
+        for (int b = 0; b < XN; ++b) {
+            const int kb = b * KC + 8 * lsub;
+            const int kc = (b < nst && kb < K) ? kb : 0;
+            gv[b] = load_cached16(na.wn + kc);
+#pragma unroll
+            for (int j = 0; j < LX; ++j) {
+                const int m = wave + WV * j;
+                const int mm = m < M ? m : M - 1;
+                xr[b][j] = load_cached16(x + (int64_t)mm * ldx + kc);
+                dr[b][j] = load_cached16(na.d + (int64_t)mm * na.ldd + kc);
+            }
+        }
+        u32x4 R[PF][LPW];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < PF; ++p) load(R[p], p < nst ? p : 0, p < nst);
+        __builtin_amdgcn_sched_barrier(0);
+        float ss[LX];
+#pragma unroll
+        for (int j = 0; j < LX; ++j) ss[j] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < XN; ++b) {
+            const int kb = b * KC + 8 * lsub;
+#pragma unroll
+            for (int j = 0; j < LX; ++j) {
+                const int m = wave + WV * j;
+                const bool live = b < nst && kb < K && m < M;
+                xr[b][j] = add_sumsq_bf16x8(live ? xr[b][j] : u32x4{0u, 0u, 0u, 0u},
+                                            live ? dr[b][j] : u32x4{0u, 0u, 0u, 0u}, ss[j]);
+            }
+        }
+        // s is kept for xout, which workgroup 0 writes after the stage loop:
+        // a store under a branch before the loop's loads would make the
+        // compiler's waits there drain every load in flight.
+#pragma unroll
+        for (int b = 0; b < XN; ++b)
+#pragma unroll
+            for (int j = 0; j < LX; ++j) sv[b][j] = xr[b][j];
+#pragma unroll
+        for (int j = 0; j < LX; ++j) {
+            wave_fold<1, 32>(&ss[j], lane);
+            const float rstd = rms_rstd(ss[j], K, na.eps);
+            const int m = wave + WV * j;
+#pragma unroll
+            for (int b = 0; b < XN; ++b) {
+                const bool live = b < nst && b * KC + 8 * lsub < K && m < M;
+                xr[b][j] = live ? normalize_bf16x8(xr[b][j], rstd, gv[b]) : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+        // Stage i: the weight rows from R[i % PF], the x rows from xr[i].
+        // All XN stages run, with no branch around a load (the compiler's
+        // waits then keep PF - 1 stages in flight); stages past K are zero
+        // (their weight registers hold placeholder loads).
+#pragma unroll
+        for (int i = 0; i < XN; ++i) {
+            u32x4 (&Rc)[LPW] = R[i % PF];
+            const bool in = i < nst;
+#pragma unroll
+            for (int j = 0; j < LPW; ++j) Rc[j] = in ? (j < LW ? Rc[j] : xr[i][j - LW]) : u32x4{0u, 0u, 0u, 0u};
+            unsigned char* const tile = smem + (i & 1) * (TR * PITCH);
+            stash(Rc, i, tile);
+            __syncthreads();  // tile i complete; every wave is done with tile i - 2
+            load(Rc, i + PF < nst ? i + PF : 0, i + PF < nst);
+            compute(tile);
+        }
+        if (blockIdx.x == 0) {
+#pragma unroll
+            for (int b = 0; b < XN; ++b) {
+                const int kb = b * KC + 8 * lsub;
+#pragma unroll
+                for (int j = 0; j < LX; ++j) {
+                    const int m = wave + WV * j;
+                    if (b < nst && kb < K && m < M) *reinterpret_cast<u32x4*>(na.xout + (int64_t)m * na.ldxo + kb) = sv[b][j];
+                }
+            }
+        }
+    } else if (sb < se) {
         const int nst = se - sb;
         u32x4 R[PF][LPW];
 #pragma unroll

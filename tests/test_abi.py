@@ -267,13 +267,17 @@ def test_normed_argument_errors(lib, kw, code, msg):
 
 
 def test_normed_fused_plans(lib):
-    """The normed plans fuse the prologue into the VALU kernel where that
-    measured fastest (qkv at M <= 4, gate_up and lm_head at M <= 2) and
+    """The normed plans fuse the prologue where that measured fastest (qkv
+    at M <= 16: VALU to M = 4, LDS-staged MFMA at 5-16; gate_up and lm_head
+    at M <= 2) and
     otherwise run the plain plan behind the separate prologue kernel
     (prologue = 1).  A VALU configuration fuses when K is unsplit, the depth
-    covers K = 2560 and there is a wave per 512-k block; prologue = 1, split
-    K and the MFMA kernels never fuse."""
-    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["qkv"], 4, 1), (QWEN["qkv"], 8, 0),
+    covers K = 2560 and there is a wave per 512-k block; an LDS-staged one
+    when K is unsplit in at most five 512-k stages with one x tile and one
+    or two weight tiles; prologue = 1, split K, the stream and the register
+    MFMA kernels never fuse."""
+    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["qkv"], 4, 1), (QWEN["qkv"], 8, 1),
+                                  (QWEN["qkv"], 16, 1), (QWEN["qkv"], 17, 0),
                                   (QWEN["gate_up"], 1, 1), (QWEN["gate_up"], 2, 1), (QWEN["gate_up"], 8, 0),
                                   (QWEN["lm_head"], 1, 1), (QWEN["lm_head"], 2, 1), (QWEN["lm_head"], 4, 0),
                                   (QWEN["gate_up"], 32, 0), (QWEN["qkv"], 32, 0), (QWEN["lm_head"], 64, 0)]:
@@ -288,9 +292,19 @@ def test_normed_fused_plans(lib):
                       (dict(n_tiles=2, waves=8, prologue=1), 0)]:
         cfg = GemmConfig(kernel=_lib.KERNEL_VALU, unroll=5, **kw)
         assert lib.krk_gemm_normed_fused(4, N, K, epi, ctypes.byref(cfg)) == fused, kw
-    for kernel in (_lib.KERNEL_STREAM, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_MFMA):
+    for kernel in (_lib.KERNEL_STREAM, _lib.KERNEL_MFMA):
         cfg = GemmConfig(kernel=kernel)
         assert lib.krk_gemm_normed_fused(16, N, K, epi, ctypes.byref(cfg)) == 0
+    # The LDS-staged kernel fuses with one 16-row x tile (M <= 16), 512-k
+    # stages, K unsplit and one or two weight tiles.
+    for M, kw, fused in [(16, dict(n_tiles=2, k_chunk=512), 1), (9, dict(n_tiles=1, k_chunk=512, unroll=3), 1),
+                         (17, dict(n_tiles=2, k_chunk=512), 0), (16, dict(n_tiles=2, k_chunk=256), 0),
+                         (16, dict(n_tiles=2, k_chunk=512, splits=2), 0), (16, dict(n_tiles=4, k_chunk=256), 0),
+                         (16, dict(n_tiles=2, k_chunk=512, prologue=1), 0)]:
+        cfg = GemmConfig(kernel=_lib.KERNEL_MFMA_LDS, **kw)
+        assert lib.krk_gemm_normed_fused(M, N, K, epi, ctypes.byref(cfg)) == fused, (M, kw)
+    cfg = GemmConfig(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=2, k_chunk=512)
+    assert lib.krk_gemm_normed_fused(16, N, 4096, epi, ctypes.byref(cfg)) == 0  # 8 stages: more than it holds
     deep = GemmConfig(kernel=_lib.KERNEL_STREAM, splits=1)
     assert lib.krk_gemm_normed_fused(8, 2560, 9728, NONE, ctypes.byref(deep)) < 0  # 19 stages: not instantiated
     bad = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=2)

@@ -862,7 +862,7 @@ def test_normed_fused_and_prologue_paths_agree(device, M, N, K, epi):
     assert ran >= 3
 
 
-@pytest.mark.parametrize("shape,M", [("qkv", M) for M in (1, 2, 3, 4)] + [("gate_up", M) for M in (1, 2)] +
+@pytest.mark.parametrize("shape,M", [("qkv", M) for M in (1, 2, 3, 4, 5, 8, 12, 16)] + [("gate_up", M) for M in (1, 2)] +
                                     [("lm_head", M) for M in (1, 2)])
 def test_normed_fused_plans_and_separate_prologue(device, shape, M):
     """Normed plans that fuse the prologue (one launch) and the same
@@ -889,22 +889,35 @@ def test_normed_fused_plans_and_separate_prologue(device, shape, M):
 
 
 def _normed_fused_configs(M, epi):
-    """VALU configurations at the fused depth: every W-rows-per-wave and wave
-    count (those with fewer waves than 512-k blocks do not fuse)."""
+    """VALU configurations at the fused depth (M <= 8): every W-rows-per-wave
+    and wave count (those with fewer waves than 512-k blocks do not fuse);
+    LDS-staged ones (M <= 16): one or two weight tiles, two or three stages
+    in flight, every channel count the tiles allow down to 8."""
     cfgs = []
-    for nt, wv in itertools.product((1, 2, 4), (2, 4, 8)):
+    if M <= 8:
+        for nt, wv in itertools.product((1, 2, 4), (2, 4, 5, 8)):
+            if epi == SILU and nt == 1:
+                continue
+            cfgs.append(dict(kernel=_lib.KERNEL_VALU, n_tiles=nt, waves=wv, unroll=5, splits=1))
+    for nt, pf in itertools.product((1, 2), (2, 3)):
         if epi == SILU and nt == 1:
             continue
-        cfgs.append(dict(kernel=_lib.KERNEL_VALU, n_tiles=nt, waves=wv, unroll=5, splits=1))
+        full = 16 * (nt // 2 if epi == SILU else nt)
+        for ch in sorted({full, max(8, full - 8)}):
+            cfgs.append(dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=nt, unroll=pf, k_chunk=512, splits=1, channels=ch))
     return cfgs
 
 
 @pytest.mark.parametrize("M,N,K,epi", [(3, 1040, 2560, NONE), (5, 600, 2048, SILU), (8, 2064, 1000, NONE),
                                        (6, 496, 2560, SILU), (8, 4100, 2560, NONE), (1, 96, 1000, SILU),
-                                       (7, 520, 2056, NONE), (2, 6144, 2560, NONE), (4, 19456, 2560, SILU)])
+                                       (7, 520, 2056, NONE), (2, 6144, 2560, NONE), (4, 19456, 2560, SILU),
+                                       (9, 1040, 2560, NONE), (12, 600, 2048, SILU), (16, 2064, 1000, NONE),
+                                       (13, 6144, 2560, NONE), (16, 19456, 2560, SILU), (11, 520, 2056, NONE),
+                                       (15, 4100, 512, SILU)])
 def test_normed_fused_configs(device, M, N, K, epi):
-    """The fused prologue under every fusing configuration, ragged K and N,
-    both epilogues, against the oracle; deterministic."""
+    """The fused prologue under every fusing configuration (VALU at M <= 8,
+    LDS-staged MFMA at M <= 16), ragged K and N, K of one to five 512-k
+    stages, both epilogues, against the oracle; deterministic."""
     x, y, wn = _norm_inputs(M, K, 9800 + M)
     w = R.randn_bf16((N, K), 9810 + M, 0.02)
     ran = 0
@@ -923,14 +936,20 @@ def test_normed_fused_configs(device, M, N, K, epi):
     assert ran >= 1
 
 
-@pytest.mark.parametrize("M,shape", [(1, "qkv"), (2, "gate_up"), (4, "qkv"), (2, "lm_head"), (8, "gate_up")])
+@pytest.mark.parametrize("M,shape", [(1, "qkv"), (2, "gate_up"), (4, "qkv"), (2, "lm_head"), (8, "gate_up"),
+                                     (12, "qkv"), (16, "gate_up"), (9, "lm_head")])
 def test_normed_fused_special_values(device, M, shape):
     """Rows with a NaN in d, an inf in x, s = x + d all zero (rstd =
     1/sqrt(eps)) and a -0 row: the fused call's NaN pattern and finite values
-    match the oracle's reference-rounded chain."""
+    match the oracle's reference-rounded chain (VALU fusion at M <= 8, the
+    LDS-staged kernel's above)."""
     K, N, epi = QWEN[shape]
-    cfg = G.normed_plan(M, N, K, epi) if G.normed_fused(M, N, K, epi) else \
-        dict(kernel=_lib.KERNEL_VALU, n_tiles=2, unroll=5, waves=8, splits=1)
+    if G.normed_fused(M, N, K, epi):
+        cfg = G.normed_plan(M, N, K, epi)
+    elif M <= 8:
+        cfg = dict(kernel=_lib.KERNEL_VALU, n_tiles=2, unroll=5, waves=8, splits=1)
+    else:
+        cfg = dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=2, unroll=2, k_chunk=512, splits=1)
     if shape == "lm_head":
         N = 4096  # lm_head's plan at its K, fewer rows to check
     assert G.normed_fused(M, N, K, epi, cfg)
@@ -985,9 +1004,11 @@ def test_add_rms_norm_kernel(device, M, K):
 def test_normed_graph_replay(device):
     """Fused and prologue-kernel normed calls captured in one graph replay to
     the eager results, with eager work between replays."""
+    lds_fused = {"kernel": _lib.KERNEL_MFMA_LDS, "n_tiles": 2, "k_chunk": 512, "splits": 1}
     cases = [(1, 6144, 2560, NONE, None), (8, 19456, 2560, SILU, None), (32, 6144, 2560, NONE, None),
              (32, 19456, 2560, SILU, None), (32, 19456, 2560, SILU, {"kernel": _lib.KERNEL_STREAM, "prologue": 1}),
-             (64, 151936, 2560, NONE, None), (2, 19456, 2560, SILU, None), (4, 6144, 2560, NONE, None)]
+             (64, 151936, 2560, NONE, None), (2, 19456, 2560, SILU, None), (4, 6144, 2560, NONE, None),
+             (12, 6144, 2560, NONE, lds_fused), (16, 19456, 2560, SILU, lds_fused)]
     ops, ins, eager, outs = [], [], [], []
     for i, (M, N, K, epi, cfg) in enumerate(cases):
         op = (G.SkinnyGateUp(M, N // 2, K, device, config=cfg) if epi == SILU
