@@ -210,11 +210,13 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx,
  *              its split-K counters must be zero before first use (every call
  *              leaves them zero); the rest is scratch.
  *
- * Fused (one launch; krk_gemm_normed_fused tells when): a VALU
- * configuration, K unsplit, at the depth that covers K = 2560 in one pass,
- * with a wave per 512-k block (K <= 512·waves).  Every workgroup then
- * normalises the rows of x itself while its first weight loads are in
- * flight (no workgroup waits for another; workgroup 0 writes xout).
+ * Fused (one launch; krk_gemm_normed_fused tells when), K unsplit: a VALU
+ * configuration at the depth that covers K = 2560 in one pass, with a wave
+ * per 512-k block (K <= 512·waves); or an MFMA_LDS configuration with
+ * k_chunk 512, K <= 2560, m_tiles 1 (M <= 16) and n_tiles <= 2.  Every
+ * workgroup then normalises the rows of x itself while its first weight
+ * loads are in flight (no workgroup waits for another; workgroup 0 writes
+ * xout).
  * Otherwise (and with prologue = 1) a one-workgroup-per-row prologue kernel
  * writes xout and the normalised rows into the workspace, then the
  * projection runs.  Both use the rounding points above.  With cfg == NULL
@@ -244,8 +246,9 @@ size_t krk_gemm_normed_workspace_bytes(int M, int N, int K, int epilogue, const 
 int krk_gemm_normed_fused(int M, int N, int K, int epilogue, const krk_gemm_config* cfg);
 
 /* The configuration krk_gemm_bf16_normed uses (the normed plan): fused where
- * that measured fastest (qkv at M <= 4, gate_up and lm_head at M <= 2 of
- * Qwen3-4B), else the plain plan with prologue = 1.  Like krk_gemm_plan it
+ * that measured fastest (qkv at M <= 16: VALU to M = 4, MFMA_LDS at 5-16;
+ * gate_up and lm_head at M <= 2 of Qwen3-4B), else the plain plan with
+ * prologue = 1.  Like krk_gemm_plan it
  * replaces the configuration pick_normed settles on
  * (engine/kernels/gemm.py:501-560).  KRK_OK or a negative code. */
 int krk_gemm_normed_plan(int M, int N, int K, int epilogue, krk_gemm_config* out);
