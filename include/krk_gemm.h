@@ -213,7 +213,8 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx,
  * Fused (one launch; krk_gemm_normed_fused tells when), K unsplit: a VALU
  * configuration at the depth that covers K = 2560 in one pass, with a wave
  * per 512-k block (K <= 512·waves); or an MFMA_LDS configuration with
- * k_chunk 512, K <= 2560, m_tiles 1 (M <= 16) and n_tiles <= 2.  Every
+ * k_chunk 512, K <= 2560, m_tiles <= 2 (M <= 32) and n_tiles <= 2 (unroll 2
+ * when both are 2).  Every
  * workgroup then normalises the rows of x itself while its first weight
  * loads are in flight (no workgroup waits for another; workgroup 0 writes
  * xout).

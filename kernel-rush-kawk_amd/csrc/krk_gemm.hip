@@ -753,15 +753,19 @@ int dispatch_valu_norm(const LaunchArgs& a, const krk_gemm_config& c, int nblock
 }
 
 // The LDS-staged kernel with the fused prologue: 512-k stages, K unsplit, one
-// 16-row x tile (the normalised rows of all stages stay in registers: with
-// two tiles the kernel spills), one or two weight tiles.
-constexpr int kLdsNormMaxMTiles = 1;
+// or two 16-row x tiles and one or two weight tiles (the normalised rows of
+// all stages stay in registers); with two of each, three stages in flight
+// would spill, so that pair runs two.
+constexpr int kLdsNormMaxMTiles = 2;
 constexpr int kLdsNormMaxNTiles = 2;
+constexpr bool lds_norm_pf3(int MT, int NT) { return MT == 1 || NT == 1; }
 
 template <int MT, int NT, bool SILU>
 int dispatch_mfma_lds_norm_pf(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s,
                               const krk::NormArgs& na) {
-    if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, true>(a, nblocks, s, {}, na);
+    if constexpr (lds_norm_pf3(MT, NT)) {
+        if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, true>(a, nblocks, s, {}, na);
+    }
     return launch_mfma_lds<MT, NT, 2, 512, SILU, false, true>(a, nblocks, s, {}, na);
 }
 
@@ -770,8 +774,10 @@ int dispatch_mfma_lds_norm(const LaunchArgs& a, const krk_gemm_config& c, int nb
                            const krk::NormArgs& na) {
     if constexpr (!SILU) {
         if (c.m_tiles == 1 && c.n_tiles == 1) return dispatch_mfma_lds_norm_pf<1, 1, false>(a, c, nblocks, s, na);
+        if (c.m_tiles == 2 && c.n_tiles == 1) return dispatch_mfma_lds_norm_pf<2, 1, false>(a, c, nblocks, s, na);
     }
     if (c.m_tiles == 1 && c.n_tiles == 2) return dispatch_mfma_lds_norm_pf<1, 2, SILU>(a, c, nblocks, s, na);
+    if (c.m_tiles == 2 && c.n_tiles == 2) return dispatch_mfma_lds_norm_pf<2, 2, SILU>(a, c, nblocks, s, na);
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS normed: m_tiles=%d n_tiles=%d", c.m_tiles, c.n_tiles);
 }
 
@@ -781,9 +787,10 @@ int dispatch_mfma_lds_norm(const LaunchArgs& a, const krk_gemm_config& c, int nb
 // reference's rounding points (krk_norm.h).  Fused, with K unsplit:
 //   * a VALU configuration at the depth covering K = 2560, with a wave per
 //     512-k block (M <= 8);
-//   * an LDS-staged MFMA configuration with 512-k stages, K <= 2560, one x
-//     tile and one or two weight tiles (M <= 16; the reference offers its
-//     fused prologue up to M = 32, engine/kernels/gemm.py:524-531).
+//   * an LDS-staged MFMA configuration with 512-k stages, K <= 2560, one or
+//     two x tiles and one or two weight tiles, two stages in flight when
+//     both are two (M <= 32; the reference offers its fused prologue up to
+//     M = 32, engine/kernels/gemm.py:524-531).
 //
 // Every workgroup of a fused call normalises all M rows itself (about ten
 // VALU instructions per element), so the fused form pays only at small M:
@@ -801,7 +808,7 @@ bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
     const int nb = cdiv(K, krk::kValuBlock);
     if (c.kernel == KRK_KERNEL_MFMA_LDS)
         return c.k_chunk == 512 && nb <= krk::kLdsNormStages && c.m_tiles <= kLdsNormMaxMTiles &&
-               c.n_tiles <= kLdsNormMaxNTiles;
+               c.n_tiles <= kLdsNormMaxNTiles && (c.unroll == 2 || lds_norm_pf3(c.m_tiles, c.n_tiles));
     if (c.kernel != KRK_KERNEL_VALU) return false;
     return c.unroll == kValuNormDepth && nb <= c.waves && krk::valu_norm_lds_bytes(c.m_tiles, nb) <= kLdsMax;
 }

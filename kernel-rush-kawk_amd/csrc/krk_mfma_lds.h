@@ -146,24 +146,17 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 
     // Stage st into registers.  Prefetches past the range read the start of
     // x row 0 instead (valid, L2-resident, never used).  The padding rows
-    // past the block's cb channels are not loaded in the plain kernel; the
-    // compiler then counts only the unconditional loads in its waits, which
-    // wait for the next stage's weight loads too (measured: loading the
-    // padding rows from x instead, so that the waits keep a whole stage in
-    // flight, made qkv and down at M = 64 3-6% slower).  With NORM every
-    // load is unconditional: there the waits in the prologue must not drain
-    // the first weight stages.
+    // past the block's cb channels are not loaded; the compiler then counts
+    // only the unconditional loads in its waits, which wait for the next
+    // stage's weight loads too (measured: loading the padding rows from x
+    // instead, so that the waits keep a whole stage in flight, made qkv and
+    // down at M = 64 3-6% slower).  NORM has its own unconditional loads.
     auto load = [&](u32x4 (&R)[LPW], int st, bool live) {
         const int kk = st * KC + 8 * lsub < K ? st * KC : -8 * lsub;  // past K: the row's start
         const int xo = 8 * lsub < K ? 8 * lsub : K - 8;
 #pragma unroll
-        for (int j = 0; j < LW; ++j) {
-            if constexpr (NORM) {
-                R[j] = load_stream16(live && rowok[j] ? rowp[j] + kk : x + xo);
-            } else {
-                R[j] = rowok[j] ? load_stream16(live ? rowp[j] + kk : x + xo) : u32x4{0u, 0u, 0u, 0u};
-            }
-        }
+        for (int j = 0; j < LW; ++j)
+            R[j] = rowok[j] ? load_stream16(live ? rowp[j] + kk : x + xo) : u32x4{0u, 0u, 0u, 0u};
         if constexpr (!NORM) {
 #pragma unroll
             for (int j = 0; j < LX; ++j) R[LW + j] = load_cached16(live ? rowp[LW + j] + kk : x + xo);
@@ -176,7 +169,6 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         for (int j = 0; j < LPW; ++j) {
             const int tr = j < LW ? RPL * (wave + WV * j) + lrow : NR + RPL * (wave + WV * (j - LW)) + lrow;
             u32x4 v = R[j];
-            if (NORM && j < LW && !rowok[j]) v = u32x4{0u, 0u, 0u, 0u};  // padding row (placeholder load)
             if (rag) v &= mk;
             *reinterpret_cast<u32x4*>(tile + tr * PITCH + 16 * (lsub ^ (tr & 15))) = v;
         }
@@ -223,10 +215,32 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 dr[b][j] = load_cached16(na.d + (int64_t)mm * na.ldd + kc);
             }
         }
-        u32x4 R[PF][LPW];
+        // Weight rows only (the x rows come from xr), every load unconditional
+        // (padding rows and stages past K read the start of x row 0 and are
+        // zeroed when staged): a load under a branch would make the waits
+        // of this prologue drain the first weight stages.
+        auto load_w = [&](u32x4 (&Rw)[LW], int st, bool live) {
+            const int kk = st * KC + 8 * lsub < K ? st * KC : -8 * lsub;
+            const int xo = 8 * lsub < K ? 8 * lsub : K - 8;
+#pragma unroll
+            for (int j = 0; j < LW; ++j) Rw[j] = load_stream16(live && rowok[j] ? rowp[j] + kk : x + xo);
+        };
+        auto stash_norm = [&](const u32x4 (&Rw)[LW], const u32x4 (&Xr)[LX], int st, bool in, unsigned char* tile) {
+            const bool rag = ragged_k && st == KST - 1;
+            const uint32_t mk = (in && st * KC + 8 * lsub < K) ? 0xffffffffu : 0u;
+#pragma unroll
+            for (int j = 0; j < LPW; ++j) {
+                const int tr = j < LW ? wave + WV * j : NR + wave + WV * (j - LW);
+                u32x4 v = j < LW ? Rw[j] : Xr[j - LW];
+                if (j < LW && !rowok[j]) v = u32x4{0u, 0u, 0u, 0u};
+                if (!in || rag) v &= mk;
+                *reinterpret_cast<u32x4*>(tile + tr * PITCH + 16 * (lsub ^ (tr & 15))) = v;
+            }
+        };
+        u32x4 RW[PF][LW];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < PF; ++p) load(R[p], p < nst ? p : 0, p < nst);
+        for (int p = 0; p < PF; ++p) load_w(RW[p], p < nst ? p : 0, p < nst);
         __builtin_amdgcn_sched_barrier(0);
         float ss[LX];
 #pragma unroll
@@ -266,14 +280,10 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         // (their weight registers hold placeholder loads).
 #pragma unroll
         for (int i = 0; i < XN; ++i) {
-            u32x4 (&Rc)[LPW] = R[i % PF];
-            const bool in = i < nst;
-#pragma unroll
-            for (int j = 0; j < LPW; ++j) Rc[j] = in ? (j < LW ? Rc[j] : xr[i][j - LW]) : u32x4{0u, 0u, 0u, 0u};
             unsigned char* const tile = smem + (i & 1) * (TR * PITCH);
-            stash(Rc, i, tile);
+            stash_norm(RW[i % PF], xr[i], i, i < nst, tile);
             __syncthreads();  // tile i complete; every wave is done with tile i - 2
-            load(Rc, i + PF < nst ? i + PF : 0, i + PF < nst);
+            load_w(RW[i % PF], i + PF < nst ? i + PF : 0, i + PF < nst);
             compute(tile);
         }
         if (blockIdx.x == 0) {

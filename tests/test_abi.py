@@ -273,9 +273,9 @@ def test_normed_fused_plans(lib):
     otherwise run the plain plan behind the separate prologue kernel
     (prologue = 1).  A VALU configuration fuses when K is unsplit, the depth
     covers K = 2560 and there is a wave per 512-k block; an LDS-staged one
-    when K is unsplit in at most five 512-k stages with one x tile and one
-    or two weight tiles; prologue = 1, split K, the stream and the register
-    MFMA kernels never fuse."""
+    when K is unsplit in at most five 512-k stages with one or two x tiles
+    and one or two weight tiles; prologue = 1, split K, the stream and the
+    register MFMA kernels never fuse."""
     for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["qkv"], 4, 1), (QWEN["qkv"], 8, 1),
                                   (QWEN["qkv"], 16, 1), (QWEN["qkv"], 17, 0),
                                   (QWEN["gate_up"], 1, 1), (QWEN["gate_up"], 2, 1), (QWEN["gate_up"], 8, 0),
@@ -295,10 +295,13 @@ def test_normed_fused_plans(lib):
     for kernel in (_lib.KERNEL_STREAM, _lib.KERNEL_MFMA):
         cfg = GemmConfig(kernel=kernel)
         assert lib.krk_gemm_normed_fused(16, N, K, epi, ctypes.byref(cfg)) == 0
-    # The LDS-staged kernel fuses with one 16-row x tile (M <= 16), 512-k
-    # stages, K unsplit and one or two weight tiles.
+    # The LDS-staged kernel fuses with one or two 16-row x tiles (M <= 32),
+    # 512-k stages, K unsplit and one or two weight tiles (with two of each,
+    # two stages in flight).
     for M, kw, fused in [(16, dict(n_tiles=2, k_chunk=512), 1), (9, dict(n_tiles=1, k_chunk=512, unroll=3), 1),
-                         (17, dict(n_tiles=2, k_chunk=512), 0), (16, dict(n_tiles=2, k_chunk=256), 0),
+                         (17, dict(n_tiles=2, k_chunk=512, unroll=2), 1), (32, dict(n_tiles=1, k_chunk=512, unroll=3), 1),
+                         (32, dict(n_tiles=2, k_chunk=512, unroll=3), 0), (33, dict(n_tiles=1, k_chunk=512), 0),
+                         (16, dict(n_tiles=2, k_chunk=256), 0),
                          (16, dict(n_tiles=2, k_chunk=512, splits=2), 0), (16, dict(n_tiles=4, k_chunk=256), 0),
                          (16, dict(n_tiles=2, k_chunk=512, prologue=1), 0)]:
         cfg = GemmConfig(kernel=_lib.KERNEL_MFMA_LDS, **kw)

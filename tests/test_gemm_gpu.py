@@ -891,8 +891,9 @@ def test_normed_fused_plans_and_separate_prologue(device, shape, M):
 def _normed_fused_configs(M, epi):
     """VALU configurations at the fused depth (M <= 8): every W-rows-per-wave
     and wave count (those with fewer waves than 512-k blocks do not fuse);
-    LDS-staged ones (M <= 16): one or two weight tiles, two or three stages
-    in flight, every channel count the tiles allow down to 8."""
+    LDS-staged ones (M <= 32): one or two weight tiles, two or three stages
+    in flight (those that do not fuse are skipped), the tiles' full channel
+    count and 8 fewer."""
     cfgs = []
     if M <= 8:
         for nt, wv in itertools.product((1, 2, 4), (2, 4, 5, 8)):
@@ -913,10 +914,11 @@ def _normed_fused_configs(M, epi):
                                        (7, 520, 2056, NONE), (2, 6144, 2560, NONE), (4, 19456, 2560, SILU),
                                        (9, 1040, 2560, NONE), (12, 600, 2048, SILU), (16, 2064, 1000, NONE),
                                        (13, 6144, 2560, NONE), (16, 19456, 2560, SILU), (11, 520, 2056, NONE),
-                                       (15, 4100, 512, SILU)])
+                                       (15, 4100, 512, SILU), (24, 1040, 2560, NONE), (32, 6144, 2560, NONE),
+                                       (20, 600, 2048, SILU), (29, 520, 1000, NONE)])
 def test_normed_fused_configs(device, M, N, K, epi):
     """The fused prologue under every fusing configuration (VALU at M <= 8,
-    LDS-staged MFMA at M <= 16), ragged K and N, K of one to five 512-k
+    LDS-staged MFMA at M <= 32), ragged K and N, K of one to five 512-k
     stages, both epilogues, against the oracle; deterministic."""
     x, y, wn = _norm_inputs(M, K, 9800 + M)
     w = R.randn_bf16((N, K), 9810 + M, 0.02)
@@ -937,7 +939,7 @@ def test_normed_fused_configs(device, M, N, K, epi):
 
 
 @pytest.mark.parametrize("M,shape", [(1, "qkv"), (2, "gate_up"), (4, "qkv"), (2, "lm_head"), (8, "gate_up"),
-                                     (12, "qkv"), (16, "gate_up"), (9, "lm_head")])
+                                     (12, "qkv"), (16, "gate_up"), (9, "lm_head"), (24, "qkv"), (32, "gate_up")])
 def test_normed_fused_special_values(device, M, shape):
     """Rows with a NaN in d, an inf in x, s = x + d all zero (rstd =
     1/sqrt(eps)) and a -0 row: the fused call's NaN pattern and finite values
@@ -1008,7 +1010,8 @@ def test_normed_graph_replay(device):
     cases = [(1, 6144, 2560, NONE, None), (8, 19456, 2560, SILU, None), (32, 6144, 2560, NONE, None),
              (32, 19456, 2560, SILU, None), (32, 19456, 2560, SILU, {"kernel": _lib.KERNEL_STREAM, "prologue": 1}),
              (64, 151936, 2560, NONE, None), (2, 19456, 2560, SILU, None), (4, 6144, 2560, NONE, None),
-             (12, 6144, 2560, NONE, lds_fused), (16, 19456, 2560, SILU, lds_fused)]
+             (12, 6144, 2560, NONE, lds_fused), (16, 19456, 2560, SILU, lds_fused),
+             (32, 6144, 2560, NONE, dict(lds_fused, unroll=2))]
     ops, ins, eager, outs = [], [], [], []
     for i, (M, N, K, epi, cfg) in enumerate(cases):
         op = (G.SkinnyGateUp(M, N // 2, K, device, config=cfg) if epi == SILU
