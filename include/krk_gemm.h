@@ -131,6 +131,13 @@ typedef struct krk_gemm_config {
                      last tile as padding (not loaded), so a shape can be cut
                      into exactly as many blocks as there are CUs.  Other
                      kernels: ignored. */
+    int x_preload; /* MFMA_LDS: 1 = x rows loaded with every stage's weight
+                     rows; 2 = x rows of the whole K loaded into registers
+                     once, before the first stage, so the stage loop loads
+                     weights only (k_chunk 512, K unsplit, K <= 2560,
+                     m_tiles <= 2, no token selection); 0 = the dispatcher's
+                     choice (the plan's when the plan uses this kernel, else
+                     1).  Other kernels: ignored. */
 } krk_gemm_config;
 
 /*

@@ -95,8 +95,8 @@ struct TableEntry {
     krk_gemm_config cfg;  // m_tiles 0: derived from M
 };
 constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, int splits, int k_chunk = 0,
-                               int channels = 0) {
-    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk, 0, channels};
+                               int channels = 0, int x_preload = 0) {
+    return krk_gemm_config{kernel, 0, n_tiles, unroll, waves, splits, k_chunk, 0, channels, x_preload};
 }
 // VALU entries: n_tiles = W rows per wave, unroll = 512-k blocks in flight per
 // row (0: enough to cover a split's K range in one pass).  MFMA_LDS entries: unroll = stages in
@@ -105,8 +105,11 @@ const TableEntry kTable[] = {
     // qkv 2560 -> 6144
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
     {6144, 2560, KRK_EPILOGUE_NONE, 2, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
-    // 256 blocks of 24 channels: one per CU, whole K
-    {6144, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1, 512, 24)},
+    // Whole K per block.  M = 9-32: x held in registers for the whole K, 192
+    // blocks of 32 channels, 3 stages in flight (1-11% faster than staging x
+    // with every stage on 256 blocks of 24); M = 33-64: 256 blocks of 24
+    // channels, one per CU, x staged per 256-k stage.
+    {6144, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32, 2)},
     {6144, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256, 24)},
     // o_proj 4096 -> 2560
     // 5-wave workgroups: 256 of 2 rows per wave at M <= 2, 512 of 1 at M = 3-6
@@ -219,6 +222,7 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
                 c->unroll = c->unroll ? c->unroll : 2;
                 c->k_chunk = c->k_chunk ? c->k_chunk : default_kc(mt, c->n_tiles);
                 c->channels = c->channels ? c->channels : 16 * (silu ? c->n_tiles / 2 : c->n_tiles);
+                c->x_preload = c->x_preload ? c->x_preload : 1;
             }
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
             if (c->kernel == KRK_KERNEL_VALU) {
@@ -261,6 +265,7 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
         r.k_chunk = default_kc(mt, r.n_tiles);
         r.waves = krk::kLdsWaves;
         r.channels = 16 * (silu ? r.n_tiles / 2 : r.n_tiles);
+        r.x_preload = 1;
         const int nblocks = cdiv(Nout, r.channels);
         r.splits = 1;
         while (nblocks * r.splits < 192 && r.splits < 4 && KST >= 2 * (r.splits + 1)) ++r.splits;
@@ -272,6 +277,12 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
 // 256 VGPRs without spilling up to this many 16-row tiles (m + n).
 constexpr int kLdsPf3MaxTiles = 6;
 constexpr bool mfma_lds_pf3(int MT, int NT) { return MT + NT <= kLdsPf3MaxTiles; }
+// MFMA_LDS with x held in registers for the whole K (x_preload = 2): 512-k
+// stages, K unsplit in at most kLdsNormStages of them, up to two x tiles.
+constexpr int kLdsXpreMaxMTiles = 2;
+inline bool lds_xpre_ok(const krk_gemm_config& c, int K) {
+    return c.k_chunk == 512 && c.splits == 1 && cdiv(K, 512) <= krk::kLdsNormStages && c.m_tiles <= kLdsXpreMaxMTiles;
+}
 
 // Dynamic LDS a gfx950 workgroup may use: 160 KB less room for the kernels'
 // static __shared__ variables.
@@ -321,6 +332,7 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
     if (c.prologue != 0 && c.prologue != 1)
         return fail(KRK_ERR_UNSUPPORTED, "prologue=%d not in {0, 1}", c.prologue);
     if (c.kernel == KRK_KERNEL_AUTO) c.kernel = a.kernel;
+    if (c.kernel != KRK_KERNEL_MFMA_LDS) c.x_preload = 0;  // MFMA_LDS only
     const bool same_kernel = c.kernel == a.kernel;
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     if (c.kernel == KRK_KERNEL_MFMA) {
@@ -369,6 +381,12 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
         if (c.channels < 8 || c.channels > full || c.channels % 8)
             return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS channels=%d: a multiple of 8 in 8..%d for %d tiles", c.channels,
                         full, c.n_tiles);
+        if (!c.x_preload) c.x_preload = same_kernel && a.x_preload == 2 && lds_xpre_ok(c, K) ? 2 : 1;
+        if (c.x_preload != 1 && c.x_preload != 2)
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=%d not in {1, 2}", c.x_preload);
+        if (c.x_preload == 2 && !lds_xpre_ok(c, K))
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=2 needs k_chunk 512, splits 1, K <= %d and m_tiles <= %d",
+                        krk::kLdsNormStages * 512, kLdsXpreMaxMTiles);
         *out = c;
         return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_STREAM) {
@@ -516,13 +534,13 @@ int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false>
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false, bool XPRE = false>
 int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::SelectArgs sa = {},
                     krk::NormArgs na = {}) {
     if constexpr ((PF == 3 && !mfma_lds_pf3(MT, NT)) || !krk::mfma_lds_kc_ok(MT, NT, KC)) {
         return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS unroll=%d k_chunk=%d with %d x %d tiles", PF, KC, MT, NT);
     } else {
-        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU, SEL, NORM>);
+        const void* fn = reinterpret_cast<const void*>(&krk::mfma_lds_kernel<MT, NT, PF, KC, SILU, SEL, NORM, XPRE>);
         const size_t shm = krk::mfma_lds_bytes(MT, NT, KC, SEL);
         // Tiles above 64 KB use gfx950's larger LDS; the limit is raised once
         // per instantiation (a function attribute, not a stream operation).
@@ -544,9 +562,23 @@ int dispatch_mfma_lds_pf(const LaunchArgs& a, const krk_gemm_config& c, int nblo
     return launch_mfma_lds<MT, NT, 2, KC, SILU>(a, nblocks, s);
 }
 
+// x held in registers for the whole K (x_preload = 2; 512-k stages).
+template <int MT, int NT, bool SILU>
+int dispatch_mfma_lds_xpre(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    if constexpr (MT <= kLdsXpreMaxMTiles && krk::mfma_lds_kc_ok(MT, NT, 512)) {
+        if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, false, true>(a, nblocks, s);
+        return launch_mfma_lds<MT, NT, 2, 512, SILU, false, false, true>(a, nblocks, s);
+    } else {
+        return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=2 with %d x %d tiles", MT, NT);
+    }
+}
+
 template <int MT, int NT, bool SILU>
 int dispatch_mfma_lds_kc(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
-    if (c.k_chunk == 512) return dispatch_mfma_lds_pf<MT, NT, 512, SILU>(a, c, nblocks, s);
+    if (c.k_chunk == 512) {
+        if (c.x_preload == 2) return dispatch_mfma_lds_xpre<MT, NT, SILU>(a, c, nblocks, s);
+        return dispatch_mfma_lds_pf<MT, NT, 512, SILU>(a, c, nblocks, s);
+    }
     return dispatch_mfma_lds_pf<MT, NT, 256, SILU>(a, c, nblocks, s);
 }
 
@@ -1497,7 +1529,11 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
             for (int kc : {256, 512})
                 for (int sp : wide_splits)
                     for (int ch : chans)
-                        if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc, 0, ch});
+                        if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc, 0, ch, 1});
+        // x held in registers for the whole K (one K split, 512-k stages).
+        for (int pf : {2, 3})
+            for (int ch : chans)
+                if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, 1, 512, 0, ch, 2});
     }
     for (int d = 2; d <= krk::kStreamMaxDepth; ++d)
         for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});

@@ -71,12 +71,15 @@ __host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool
 // keeps the normalised rows in registers, from which every stage's x rows
 // are staged; no x loads remain in the loop.  Workgroup 0 writes s to
 // na.xout after the loop.
+// XPRE: the same register-held x rows without the prologue: x for the whole
+// K (at most kLdsNormStages 512-k stages, K unsplit) is loaded once before
+// the first stage, and the stage loop loads weights only.
 // cb: output channels per block (a multiple of 8, at most 16·NH).  Below
 // 16·NH the last tile is partly padding: its rows past cb are not loaded
 // (zeros in the tile) and their outputs not stored.  This lets a shape use
 // all 256 CUs with whole K (qkv: 6144 = 256 x 24 channels) instead of
 // leaving CUs idle or splitting K.
-template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false>
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false, bool XPRE = false>
 __global__ void __launch_bounds__(64 * kLdsWaves)
 mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const uint16_t* __restrict__ w, int64_t ldw,
@@ -84,7 +87,8 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 int M, int N, int K, int splits, int cb,
                 float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa, NormArgs na) {
     static_assert(!(SEL && SILU), "selection reads plain logits");
-    static_assert(!NORM || (KC == 512 && !SEL), "the fused prologue stages whole 512-k x rows");
+    static_assert(!(NORM || XPRE) || (KC == 512 && !SEL), "x rows held in registers are whole 512-k rows");
+    static_assert(!(NORM && XPRE), "the fused prologue already holds x in registers");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     static_assert(!SILU || (NT % 2 == 0), "SILU pairs gate and up tiles");
     static_assert(PF >= 2, "at least two stages in flight");
@@ -194,7 +198,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         }
     };
 
-    if constexpr (NORM) {
+    if constexpr (NORM || XPRE) {
         // K unsplit (sb = 0) in nst <= XN stages of 512: lane l of wave w
         // holds k = 512·b + 8l of rows w + 8j for every stage b.  Rows past
         // M and k past K are zero.
@@ -206,13 +210,13 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         for (int b = 0; b < XN; ++b) {
             const int kb = b * KC + 8 * lsub;
             const int kc = (b < nst && kb < K) ? kb : 0;
-            gv[b] = load_cached16(na.wn + kc);
+            if constexpr (NORM) gv[b] = load_cached16(na.wn + kc);
 #pragma unroll
             for (int j = 0; j < LX; ++j) {
                 const int m = wave + WV * j;
                 const int mm = m < M ? m : M - 1;
                 xr[b][j] = load_cached16(x + (int64_t)mm * ldx + kc);
-                dr[b][j] = load_cached16(na.d + (int64_t)mm * na.ldd + kc);
+                if constexpr (NORM) dr[b][j] = load_cached16(na.d + (int64_t)mm * na.ldd + kc);
             }
         }
         // Weight rows only (the x rows come from xr), every load unconditional
@@ -242,37 +246,49 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
         for (int p = 0; p < PF; ++p) load_w(RW[p], p < nst ? p : 0, p < nst);
         __builtin_amdgcn_sched_barrier(0);
-        float ss[LX];
+        if constexpr (NORM) {
+            float ss[LX];
 #pragma unroll
-        for (int j = 0; j < LX; ++j) ss[j] = 0.0f;
-#pragma unroll
-        for (int b = 0; b < XN; ++b) {
-            const int kb = b * KC + 8 * lsub;
-#pragma unroll
-            for (int j = 0; j < LX; ++j) {
-                const int m = wave + WV * j;
-                const bool live = b < nst && kb < K && m < M;
-                xr[b][j] = add_sumsq_bf16x8(live ? xr[b][j] : u32x4{0u, 0u, 0u, 0u},
-                                            live ? dr[b][j] : u32x4{0u, 0u, 0u, 0u}, ss[j]);
-            }
-        }
-        // s is kept for xout, which workgroup 0 writes after the stage loop:
-        // a store under a branch before the loop's loads would make the
-        // compiler's waits there drain every load in flight.
-#pragma unroll
-        for (int b = 0; b < XN; ++b)
-#pragma unroll
-            for (int j = 0; j < LX; ++j) sv[b][j] = xr[b][j];
-#pragma unroll
-        for (int j = 0; j < LX; ++j) {
-            wave_fold<1, 32>(&ss[j], lane);
-            const float rstd = rms_rstd(ss[j], K, na.eps);
-            const int m = wave + WV * j;
+            for (int j = 0; j < LX; ++j) ss[j] = 0.0f;
 #pragma unroll
             for (int b = 0; b < XN; ++b) {
-                const bool live = b < nst && b * KC + 8 * lsub < K && m < M;
-                xr[b][j] = live ? normalize_bf16x8(xr[b][j], rstd, gv[b]) : u32x4{0u, 0u, 0u, 0u};
+                const int kb = b * KC + 8 * lsub;
+#pragma unroll
+                for (int j = 0; j < LX; ++j) {
+                    const int m = wave + WV * j;
+                    const bool live = b < nst && kb < K && m < M;
+                    xr[b][j] = add_sumsq_bf16x8(live ? xr[b][j] : u32x4{0u, 0u, 0u, 0u},
+                                                live ? dr[b][j] : u32x4{0u, 0u, 0u, 0u}, ss[j]);
+                }
             }
+            // s is kept for xout, which workgroup 0 writes after the stage loop:
+            // a store under a branch before the loop's loads would make the
+            // compiler's waits there drain every load in flight.
+#pragma unroll
+            for (int b = 0; b < XN; ++b)
+#pragma unroll
+                for (int j = 0; j < LX; ++j) sv[b][j] = xr[b][j];
+#pragma unroll
+            for (int j = 0; j < LX; ++j) {
+                wave_fold<1, 32>(&ss[j], lane);
+                const float rstd = rms_rstd(ss[j], K, na.eps);
+                const int m = wave + WV * j;
+#pragma unroll
+                for (int b = 0; b < XN; ++b) {
+                    const bool live = b < nst && b * KC + 8 * lsub < K && m < M;
+                    xr[b][j] = live ? normalize_bf16x8(xr[b][j], rstd, gv[b]) : u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        } else {
+            // XPRE: rows past M and k past K (whole stages past K, and the
+            // ragged tail, masked when staged) are zero.
+#pragma unroll
+            for (int b = 0; b < XN; ++b)
+#pragma unroll
+                for (int j = 0; j < LX; ++j) {
+                    const bool live = b < nst && wave + WV * j < M;
+                    xr[b][j] = live ? xr[b][j] : u32x4{0u, 0u, 0u, 0u};
+                }
         }
         // Stage i: the weight rows from R[i % PF], the x rows from xr[i].
         // All XN stages run, with no branch around a load (the compiler's
@@ -286,7 +302,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             load_w(RW[i % PF], i + PF < nst ? i + PF : 0, i + PF < nst);
             compute(tile);
         }
-        if (blockIdx.x == 0) {
+        if (NORM && blockIdx.x == 0) {
 #pragma unroll
             for (int b = 0; b < XN; ++b) {
                 const int kb = b * KC + 8 * lsub;

@@ -41,7 +41,8 @@ _size = ctypes.c_size_t
 
 
 class GemmConfig(ctypes.Structure):
-    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk, prologue, channels."""
+    """``krk_gemm_config``: kernel, m_tiles, n_tiles, unroll, waves, splits, k_chunk, prologue, channels,
+    x_preload."""
 
     _fields_ = [
         ("kernel", _int),
@@ -53,6 +54,7 @@ class GemmConfig(ctypes.Structure):
         ("k_chunk", _int),
         ("prologue", _int),
         ("channels", _int),
+        ("x_preload", _int),
     ]
 
     def as_dict(self) -> dict:

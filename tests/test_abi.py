@@ -145,6 +145,26 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
         assert blocks >= 150, f"{shape} M={M}: {blocks} workgroups ({c})"
 
 
+def test_x_preload_resolution(lib):
+    """x_preload resolves to the plan's choice for MFMA_LDS (2 for qkv at
+    M = 9-32, 1 at 33-64 and where x cannot be held), to 0 for the other
+    kernels, and a caller's 1 or 2 is kept where it is valid."""
+    def resolve(M, N, K, **kw):
+        out = GemmConfig()
+        assert lib.krk_gemm_resolve(M, N, K, NONE, ctypes.byref(GemmConfig.from_dict(kw)), ctypes.byref(out)) == 0
+        return out.as_dict()
+    assert resolve(12, 6144, 2560)["x_preload"] == 2
+    assert resolve(20, 6144, 2560)["x_preload"] == 2
+    assert resolve(32, 6144, 2560)["x_preload"] == 2
+    assert resolve(33, 6144, 2560)["x_preload"] == 1
+    assert resolve(12, 6144, 2560, kernel=3, k_chunk=256)["x_preload"] == 1  # the plan's 2 does not apply
+    assert resolve(12, 6144, 2560, kernel=3, x_preload=1)["x_preload"] == 1
+    assert resolve(24, 6144, 2560, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2
+    assert resolve(40, 2560, 4096, kernel=3)["x_preload"] == 1  # o: 8 stages of 512
+    for kernel in (1, 2, 5):
+        assert resolve(8, 6144, 2560, kernel=kernel, x_preload=2)["x_preload"] == 0
+
+
 @pytest.mark.parametrize("cfg,code,msg", [
     (dict(kernel=9), _lib.KRK_ERR_UNSUPPORTED, "unknown kernel"),
     (dict(kernel=1, m_tiles=1), _lib.KRK_ERR_INVALID, "cannot cover"),
@@ -158,6 +178,10 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
     (dict(kernel=3, waves=4), _lib.KRK_ERR_UNSUPPORTED, "waves"),
     (dict(kernel=3, m_tiles=2, n_tiles=4, k_chunk=512), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
     (dict(kernel=3, k_chunk=384), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
+    (dict(kernel=3, x_preload=3), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
+    (dict(kernel=3, k_chunk=256, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
+    (dict(kernel=3, k_chunk=512, n_tiles=2, splits=2, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
+    (dict(kernel=3, m_tiles=3, n_tiles=1, k_chunk=256, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
 ])
 def test_config_errors(lib, cfg, code, msg):
     c = GemmConfig.from_dict(cfg)

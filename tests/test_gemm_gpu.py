@@ -285,6 +285,7 @@ SPECIAL_FAMILIES = [
     ("lds-staged", 16, dict(kernel=_lib.KERNEL_MFMA_LDS, splits=1)),
     ("lds-staged split-K", 24, dict(kernel=_lib.KERNEL_MFMA_LDS, splits=3)),
     ("lds-staged 24 channels split-K", 20, dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=4, channels=24, splits=2)),
+    ("lds-staged x in registers", 20, dict(kernel=_lib.KERNEL_MFMA_LDS, n_tiles=2, k_chunk=512, splits=1, x_preload=2)),
     ("stream", 33, dict(kernel=_lib.KERNEL_STREAM, splits=1)),
     ("stream split-K", 8, dict(kernel=_lib.KERNEL_STREAM, splits=2)),
     ("register mfma split-K", 13, dict(kernel=_lib.KERNEL_MFMA, splits=2)),
@@ -515,6 +516,33 @@ def test_lds_partial_channel_configs(device, M, N, K, epi):
     x = R.randn_bf16((M, K), 8750 + M)
     w = R.randn_bf16((N, K), 8751 + N, 0.02)
     _run_configs(x, w, epi, _lds_channel_configs(M, epi == SILU))
+
+
+def _lds_xpre_configs(M, silu):
+    """LDS-staged configurations that hold x in registers for the whole K
+    (x_preload = 2): one or two x tiles, one or two weight tiles, two or
+    three stages in flight, all of the tiles' channels and 8 fewer."""
+    mt_min = -(-min(M, 64) // 16)
+    for mt, nt, pf in itertools.product(range(mt_min, 3), (1, 2), (2, 3)):
+        if silu and nt % 2:
+            continue
+        full = 16 * (nt // 2 if silu else nt)
+        for ch in sorted({full, max(8, full - 8)}):
+            yield dict(kernel=_lib.KERNEL_MFMA_LDS, m_tiles=mt, n_tiles=nt, unroll=pf, k_chunk=512, splits=1,
+                       channels=ch, x_preload=2)
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(1, 96, 1536, NONE), (9, 200, 1000, NONE), (16, 6144, 2560, NONE),
+                                       (24, 520, 2056, NONE), (32, 130, 512, NONE), (3, 96, 8, NONE),
+                                       (13, 2 * 96, 2560, SILU), (20, 2 * 200, 1032, SILU), (32, 2 * 600, 2048, SILU)])
+def test_lds_x_in_registers_configs(device, M, N, K, epi):
+    """x held in registers for the whole K (one to five 512-k stages, ragged
+    K down to a single 8-element chunk, ragged N, partial channel blocks,
+    both epilogues) gives the oracle's results, and the same as staging x
+    with every stage within the fp32 bound."""
+    x = R.randn_bf16((M, K), 8780 + M)
+    w = R.randn_bf16((N, K), 8781 + N, 0.02)
+    _run_configs(x, w, epi, _lds_xpre_configs(M, epi == SILU))
 
 
 @pytest.mark.parametrize("kernel", [_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_VALU])
