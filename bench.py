@@ -248,6 +248,10 @@ def main() -> int:
                 op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
                 ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
                 calls = [(lambda w=w: op.run(xt, w, ot)) for w in wsh]
+                # The shard's weights are fresh allocations: one untimed pass
+                # first (the first pass over them measured up to 20% slower,
+                # whichever configuration ran it).
+                replay_ms(calls, reps=1)
                 ms = replay_ms(calls)
                 B.start(3.0)
                 try:

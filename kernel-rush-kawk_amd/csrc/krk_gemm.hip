@@ -143,16 +143,15 @@ const TableEntry kTable[] = {
     // One GPU's shard under 8-way tensor parallelism (QKV, gate_up and
     // lm_head split along N, o and down along K), from the warm-up tuner's
     // full search on an MI355X (graph replay over >= 300 MB of weight copies).
-    // qkv shard 2560 -> 768
+    // qkv shard 2560 -> 768 (M = 9-32: x held in registers, 8-17% faster)
     {768, 2560, KRK_EPILOGUE_NONE, 1, 8, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
-    {768, 2560, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
-    {768, 2560, KRK_EPILOGUE_NONE, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
-    {768, 2560, KRK_EPILOGUE_NONE, 25, 48, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 3, 256)},
-    {768, 2560, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 4, 256)},
+    {768, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512, 16, 2)},
+    {768, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 4, 256)},
     // o shard 512 -> 2560
     {2560, 512, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
     {2560, 512, KRK_EPILOGUE_NONE, 2, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
-    {2560, 512, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
+    {2560, 512, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
+    {2560, 512, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA, 1, 4, 4, 1)},
     {2560, 512, KRK_EPILOGUE_NONE, 17, 48, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
     {2560, 512, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
     // gate_up shard 2560 -> 2 x 1216 with SiLU*mul
@@ -160,16 +159,13 @@ const TableEntry kTable[] = {
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 2, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 9, 16, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
-    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3, 256)},
-    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 25, 32, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
+    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1, 512, 8)},
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3, 256)},
     // down shard 1216 -> 2560
     {2560, 1216, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {2560, 1216, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
     {2560, 1216, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
-    {2560, 1216, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 256)},
-    {2560, 1216, KRK_EPILOGUE_NONE, 17, 24, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
-    {2560, 1216, KRK_EPILOGUE_NONE, 25, 48, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 256)},
+    {2560, 1216, KRK_EPILOGUE_NONE, 5, 48, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 256)},
     {2560, 1216, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
     // lm_head shard 2560 -> 18992
     {18992, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 4, 1)},
