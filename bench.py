@@ -30,6 +30,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "kernel-rush-kawk_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+# Calls per timed graph in the per-shape tables (the weights cycle through
+# the available copies): a graph replay costs ~10 us beyond its kernels, which
+# over 4 calls adds 2.5 us to each (lm_head with its 2 weight copies).
+MIN_CALLS = 32
 HIDDEN, INTER, VOCAB, LAYERS, QW = 2560, 9728, 151936, 36, 4096
 # name -> (K, N_w, silu)
 SHAPES = {
@@ -207,7 +211,7 @@ def main() -> int:
                 op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
                 ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
                 ws = lm if name == "lm_head" else [L[name] for L in layers]
-                n = 2 * len(ws) if name == "lm_head" else len(ws)
+                n = max(MIN_CALLS, len(ws))
                 calls = [(lambda w=ws[i % len(ws)]: op.run(xt, w, ot)) for i in range(n)]
                 ms = replay_ms(calls)
                 row = {"shape": name, "M": Mt, "us": round(ms * 1000, 2),
@@ -247,11 +251,8 @@ def main() -> int:
                 epi = G.EPILOGUE_SILU_MUL if silu else G.EPILOGUE_NONE
                 op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
                 ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
-                calls = [(lambda w=w: op.run(xt, w, ot)) for w in wsh]
-                # The shard's weights are fresh allocations: one untimed pass
-                # first (the first pass over them measured up to 20% slower,
-                # whichever configuration ran it).
-                replay_ms(calls, reps=1)
+                n = max(MIN_CALLS, len(wsh))
+                calls = [(lambda w=wsh[i % len(wsh)]: op.run(xt, w, ot)) for i in range(n)]
                 ms = replay_ms(calls)
                 B.start(3.0)
                 try:
@@ -265,9 +266,10 @@ def main() -> int:
                        "tuned_us": round(tuned.us, 2), "tuned_config": tuned.config, "candidates_timed": len(tuned.trials)}
                 if not args.no_torch:
                     if silu:
-                        tc = [(lambda w=w: (lambda r: F.silu(r[:, :Nw // 2]) * r[:, Nw // 2:])(F.linear(xt, w))) for w in wsh]
+                        tc = [(lambda w=wsh[i % len(wsh)]: (lambda r: F.silu(r[:, :Nw // 2]) * r[:, Nw // 2:])(F.linear(xt, w)))
+                              for i in range(n)]
                     else:
-                        tc = [(lambda w=w: F.linear(xt, w)) for w in wsh]
+                        tc = [(lambda w=wsh[i % len(wsh)]: F.linear(xt, w)) for i in range(n)]
                     tms = replay_ms(tc)
                     row["torch_gpu_us"] = round(tms * 1000, 2)
                 shards.append(row)
@@ -295,7 +297,7 @@ def main() -> int:
                 op = G.SkinnyGateUp(Mt, Nw // 2, K, dev) if silu else G.SkinnyMatmul(Mt, Nw, K, dev)
                 ot = torch.empty((Mt, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)
                 ws = lm if name == "lm_head" else [L[name] for L in layers]
-                n = 2 * len(ws) if name == "lm_head" else len(ws)
+                n = max(MIN_CALLS, len(ws))
                 fused_ms = replay_ms([(lambda w=ws[i % len(ws)]: op.run(xt, w, ot, norm=(yt, wn, xo, eps)))
                                                     for i in range(n)])
                 two_ms = replay_ms([(lambda w=ws[i % len(ws)]: op.run(G.add_rms_norm(xt, yt, wn, eps, xout=xo), w, ot))
@@ -336,7 +338,7 @@ def main() -> int:
             for k in (1, 8):
                 op = G.SkinnySelect(Mt, Nw, K, dev, k)
                 idx = torch.empty((Mt, k), dtype=torch.int64, device=dev)
-                n = 2 * len(lm)
+                n = max(MIN_CALLS, len(lm))
                 f_ms = replay_ms([(lambda w=lm[i % len(lm)]: op.run(xt, w, idx)) for i in range(n)])
                 if k == 1:
                     sel = lambda: torch.argmax(lg, dim=-1)
