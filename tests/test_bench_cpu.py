@@ -26,3 +26,23 @@ def test_a_multi_rank_launch_is_refused():
     env = dict(os.environ, WORLD_SIZE="4", RANK="0", LOCAL_RANK="0")
     r = _run("--gpus", "1", env=env)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_traffic_record_matches_the_dominant_plan():
+    """The committed rocprofv3 traffic record is on the configuration the
+    dispatch table picks for the headline's dominant kernel (gate_up at
+    M = 32), so bench.py's roofline.traffic is filled, not null."""
+    import importlib.util
+    import json
+
+    sys.path.insert(0, str(ROOT / "kernel-rush-kawk_amd"))
+    from kernels import gemm as G
+
+    spec = importlib.util.spec_from_file_location("bench_mod", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    rec = json.loads(bench.TRAFFIC_FILE.read_text())
+    cfg = G.plan(32, 19456, 2560, G.EPILOGUE_SILU_MUL)
+    assert rec["config"] == cfg
+    assert bench.measured_traffic("gate_up", 32, cfg) == rec["traffic_bytes_per_launch"]
+    assert 1.0 <= rec["traffic_bytes_per_launch"] / rec["algorithmic_bytes_per_launch"] < 1.1
