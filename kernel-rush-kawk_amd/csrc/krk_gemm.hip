@@ -104,12 +104,14 @@ constexpr krk_gemm_config kcfg(int kernel, int n_tiles, int unroll, int waves, i
 const TableEntry kTable[] = {
     // qkv 2560 -> 6144
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 2, 8, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
-    // Whole K per block.  M = 9-32: x held in registers for the whole K, 192
+    {6144, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
+    // Whole K per block.  M = 5-32: x held in registers for the whole K, 192
     // blocks of 32 channels, 3 stages in flight (1-11% faster than staging x
-    // with every stage on 256 blocks of 24); M = 33-64: 256 blocks of 24
-    // channels, one per CU, x staged per 256-k stage.
-    {6144, 2560, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32, 2)},
+    // with every stage on 256 blocks of 24 at M = 9-32, 3-6% faster than the
+    // VALU kernel at M = 5-8); M = 33-64: 256 blocks of 24 channels, one per
+    // CU, x staged per 256-k stage.
+    {6144, 2560, KRK_EPILOGUE_NONE, 5, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32, 2)},
     {6144, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256, 24)},
     // o_proj 4096 -> 2560
     // 5-wave workgroups: 256 of 2 rows per wave at M <= 2, 512 of 1 at M = 3-6
@@ -130,7 +132,7 @@ const TableEntry kTable[] = {
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 5, 1)},
     {2560, 9728, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 2, 8, 3)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 4, 5, 1)},
     {2560, 9728, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
     {2560, 9728, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 6, 256)},
     {2560, 9728, KRK_EPILOGUE_NONE, 17, 48, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
@@ -139,7 +141,9 @@ const TableEntry kTable[] = {
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
-    {151936, 2560, KRK_EPILOGUE_NONE, 5, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    // 7 stages in the ring with one x tile (4-5% faster than 5), 5 with two
+    {151936, 2560, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_STREAM, 1, 7, 0, 1)},
+    {151936, 2560, KRK_EPILOGUE_NONE, 17, 32, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
 
     // One GPU's shard under 8-way tensor parallelism (QKV, gate_up and
@@ -1092,11 +1096,19 @@ struct SelectPlan {
     bool fused;
 };
 
+// Ring depth of the plan's stream kernel when it selects tokens: the
+// selecting variants keep their running keys in registers and measured
+// fastest with 5 stages (lm_head M = 5-16: 116 against 119 µs for argmax,
+// 122 against 131 µs for top-8 with the 7 the plain plan uses).
+constexpr int kStreamSelDepth = 5;
+
 int select_plan_for(int M, int N, int K, int k, const krk_gemm_config* cfg, SelectPlan* out) {
     const int Mc = M < kMaxRowsPerLaunch ? M : kMaxRowsPerLaunch;
     int rc = resolve_config(M, N, K, KRK_EPILOGUE_NONE, cfg, &out->c);
     if (rc) return rc;
     out->fused = select_fusable(out->c, Mc, K, k);
+    if (!cfg && out->fused && out->c.kernel == KRK_KERNEL_STREAM && out->c.unroll > kStreamSelDepth)
+        out->c.unroll = kStreamSelDepth;
     return KRK_OK;
 }
 

@@ -13,6 +13,7 @@ library's own.
 from __future__ import annotations
 
 import itertools
+import math
 import statistics
 from typing import Callable, Sequence
 
@@ -48,10 +49,22 @@ class GraphReplay:
     def replay(self) -> None:
         self.graph.replay()
 
-    def ms_per_call(self, reps: int = 5) -> float:
+    def ms_per_call(self, reps: int = 5, warm_ms: float = 10.0) -> float:
         """Median over ``reps`` timed replays, divided by the number of calls.
-        The replays are enqueued back to back and read after one
-        synchronisation."""
+        Untimed replays covering about ``warm_ms`` of GPU time run first: a
+        GPU that idled while the graph was built runs its first milliseconds
+        slower (measured on an MI355X: with one untimed replay, the first of
+        several timings of a graph came out up to 8% above the rest, with
+        2 ms of replays up to 3%, with 10 ms within 0.5%).  The timed replays
+        are enqueued back to back and read after one synchronisation."""
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        self.replay()
+        end.record()
+        torch.cuda.synchronize()
+        one = max(begin.elapsed_time(end), 1e-3)
+        for _ in range(min(64, math.ceil(warm_ms / one))):
+            self.replay()
         marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for begin, end in marks:
             begin.record()

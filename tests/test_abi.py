@@ -71,8 +71,8 @@ def test_argument_errors(lib, kw, code, msg):
 
 
 def _split_shape(lib):
-    """A shape whose plan splits K (down_proj at M = 4) and its workspace size."""
-    M, N, K = 4, 2560, 9728
+    """A shape whose plan splits K (down_proj at M = 8) and its workspace size."""
+    M, N, K = 8, 2560, 9728
     cfg = GemmConfig()
     assert lib.krk_gemm_plan(M, N, K, NONE, ctypes.byref(cfg)) == 0 and cfg.splits > 1
     need = lib.krk_gemm_workspace_bytes(M, N, K, NONE)
@@ -425,7 +425,8 @@ def _stream_groups(nblocks, cus=256):
 
 
 def test_select_plan_and_workspace(lib):
-    """The projection plan is the plain table's; argmax fuses into the VALU
+    """The projection plan is the plain table's (a fusing stream plan keeps a
+    ring of at most 5 stages); argmax fuses into the VALU
     (M <= 4) and stream (from M = 5, K of 5 stages) plans and into
     LDS-staged MFMA configurations; top-k fuses into stream plans of up to
     16 rows only.  Workspace: the row counters, then the keys of each row
@@ -442,9 +443,11 @@ def test_select_plan_and_workspace(lib):
             cfg, plain = GemmConfig(), GemmConfig()
             assert lib.krk_gemm_select_plan(M, N, K, k, ctypes.byref(cfg)) == 0
             assert lib.krk_gemm_plan(M, N, K, NONE, ctypes.byref(plain)) == 0
-            c = cfg.as_dict()
-            assert c == plain.as_dict() and c["kernel"] == kernel, (M, k, c)
+            c, p = cfg.as_dict(), plain.as_dict()
             fused = lib.krk_gemm_select_fused(M, N, K, k, None)
+            if fused and kernel == _lib.KERNEL_STREAM:
+                p["unroll"] = min(p["unroll"], 5)
+            assert c == p and c["kernel"] == kernel, (M, k, c)
             assert fused == int(k == 1 or (kernel == _lib.KERNEL_STREAM and Mc <= 16)), (M, k)
             if fused:
                 G = -(-N // _channels_per_block(c, NONE))
