@@ -494,7 +494,8 @@ def profile_shape(torch, G, dev, name: str, M: int) -> int:
     projection over distinct weights (the 36 layer weights of the sweep; for
     lm_head 2 copies, 8 launches), then 4 copies of a 256 MiB buffer for the
     counters' byte calibration.  Prints the configuration and the event-timed
-    µs per launch of the graph (median of 3 replays after 9 untimed ones)."""
+    µs per launch of the graph (median of 3 replays, after the timer's ~10 ms
+    of untimed ones)."""
     K, Nw, silu = SHAPES[name]
     if name == "lm_head":
         ws = [randn_bf16(torch, (Nw, K), seed_for(4, 99, "lm_head") + i, 0.02, dev) for i in range(2)] * 4
@@ -507,9 +508,7 @@ def profile_shape(torch, G, dev, name: str, M: int) -> int:
     from kernels.timing import GraphReplay
 
     replay = GraphReplay(calls)  # 3 eager warm-up calls, then the capture and one replay
-    for _ in range(8):  # bring the clocks up before the timed replays
-        replay.replay()
-    ms = replay.ms_per_call(reps=3)
+    ms = replay.ms_per_call(reps=3)  # untimed replays first bring the clocks up
     a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
     for _ in range(4):
@@ -517,7 +516,7 @@ def profile_shape(torch, G, dev, name: str, M: int) -> int:
     torch.cuda.synchronize()
     print(json.dumps({"profile": name, "shape": name, "M": M, "config": op.resolved_config,
                       "kernel": KERNEL_NAMES[op.resolved_config["kernel"]], "us_per_launch": round(ms * 1000, 3),
-                      "algorithmic_bytes": algo_bytes(name, M), "launches": len(calls) * 12 + 3,
+                      "algorithmic_bytes": algo_bytes(name, M), "launches_per_replay": len(calls),
                       "copy_bytes": 256 << 20, "copies": 4}), flush=True)
     return 0
 
