@@ -156,13 +156,12 @@ const TableEntry kTable[] = {
     // o shard 512 -> 2560
     {2560, 512, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
     {2560, 512, KRK_EPILOGUE_NONE, 2, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
-    {2560, 512, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
-    {2560, 512, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA, 1, 4, 4, 1)},
+    {2560, 512, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA, 1, 4, 4, 1)},
     {2560, 512, KRK_EPILOGUE_NONE, 17, 48, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 512)},
     {2560, 512, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 1, 2, 0, 1, 256)},
     // gate_up shard 2560 -> 2 x 1216 with SiLU*mul
-    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
-    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 2, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
+    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 1, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 5, 1)},
+    {2432, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 9, 16, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     {2432, 2560, KRK_EPILOGUE_SILU_MUL, 17, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 1, 512, 8)},
