@@ -227,8 +227,11 @@ int krk_gemm_bf16_config(const void* x, int64_t ldx,
  * xout).
  * Otherwise (and with prologue = 1) a one-workgroup-per-row prologue kernel
  * writes xout and the normalised rows into the workspace, then the
- * projection runs.  Both use the rounding points above.  With cfg == NULL
- * the call uses krk_gemm_normed_plan.
+ * projection runs; in front of a STREAM projection of at most 64 rows the
+ * rows go in that kernel's MFMA fragment order (padded to 16-row tiles and
+ * whole 512-k stages), so that it loads them as whole 1 KB runs and skips
+ * their trip through LDS.  Both use the rounding points above.  With
+ * cfg == NULL the call uses krk_gemm_normed_plan.
  */
 int krk_gemm_bf16_normed(const void* x, int64_t ldx, const void* d, int64_t ldd,
                          const void* w_norm, float eps, void* xout, int64_t ldxo,

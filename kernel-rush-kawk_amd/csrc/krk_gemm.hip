@@ -604,9 +604,9 @@ int dispatch_mfma_lds(const LaunchArgs& a, const krk_gemm_config& c, int nblocks
     return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int XS, bool SILU, int SK = 0>
+template <int MT, int XS, bool SILU, int SK = 0, bool XF = false>
 int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {}) {
-    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK>);
+    const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK, XF>);
     int nred = stream_nred_for(a.K, a.splits);
     size_t shm = krk::stream_lds_bytes(MT, depth, nred);
     const int G = stream_groups(nblocks, a.splits);
@@ -632,26 +632,26 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     return hip_status(e, "stream_gemm_kernel launch");
 }
 
-template <int MT, bool SILU>
+template <int MT, bool SILU, bool XF = false>
 int dispatch_stream_xs(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
     const int xs = stream_xs(MT, cdiv(cdiv(a.K, krk::kStreamKC), c.splits));
     if constexpr (MT == 1) {
         switch (xs) {
-            case 4: return launch_stream<1, 4, SILU>(a, nblocks, c.unroll, s);
-            case 5: return launch_stream<1, 5, SILU>(a, nblocks, c.unroll, s);
-            case 8: return launch_stream<1, 8, SILU>(a, nblocks, c.unroll, s);
-            case 10: return launch_stream<1, 10, SILU>(a, nblocks, c.unroll, s);
+            case 4: return launch_stream<1, 4, SILU, 0, XF>(a, nblocks, c.unroll, s);
+            case 5: return launch_stream<1, 5, SILU, 0, XF>(a, nblocks, c.unroll, s);
+            case 8: return launch_stream<1, 8, SILU, 0, XF>(a, nblocks, c.unroll, s);
+            case 10: return launch_stream<1, 10, SILU, 0, XF>(a, nblocks, c.unroll, s);
         }
     } else if constexpr (MT == 2) {
         switch (xs) {
-            case 4: return launch_stream<2, 4, SILU>(a, nblocks, c.unroll, s);
-            case 5: return launch_stream<2, 5, SILU>(a, nblocks, c.unroll, s);
-            case 8: return launch_stream<2, 8, SILU>(a, nblocks, c.unroll, s);
+            case 4: return launch_stream<2, 4, SILU, 0, XF>(a, nblocks, c.unroll, s);
+            case 5: return launch_stream<2, 5, SILU, 0, XF>(a, nblocks, c.unroll, s);
+            case 8: return launch_stream<2, 8, SILU, 0, XF>(a, nblocks, c.unroll, s);
         }
     } else {
         switch (xs) {
-            case 4: return launch_stream<MT, 4, SILU>(a, nblocks, c.unroll, s);
-            case 5: return launch_stream<MT, 5, SILU>(a, nblocks, c.unroll, s);
+            case 4: return launch_stream<MT, 4, SILU, 0, XF>(a, nblocks, c.unroll, s);
+            case 5: return launch_stream<MT, 5, SILU, 0, XF>(a, nblocks, c.unroll, s);
         }
     }
     return fail(KRK_ERR_UNSUPPORTED, "STREAM has no x-register layout for m_tiles=%d and this K split", MT);
@@ -679,13 +679,14 @@ int dispatch_stream_sel(const LaunchArgs& a, const krk_gemm_config& c, int nbloc
     return fail(KRK_ERR_UNSUPPORTED, "STREAM selection epilogue: m_tiles=%d", c.m_tiles);
 }
 
+// xf: x in the kernel's fragment order (a normed call's prologue wrote it).
 template <bool SILU>
-int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s, bool xf = false) {
     switch (c.m_tiles) {
-        case 1: return dispatch_stream_xs<1, SILU>(a, c, nblocks, s);
-        case 2: return dispatch_stream_xs<2, SILU>(a, c, nblocks, s);
-        case 3: return dispatch_stream_xs<3, SILU>(a, c, nblocks, s);
-        case 4: return dispatch_stream_xs<4, SILU>(a, c, nblocks, s);
+        case 1: return xf ? dispatch_stream_xs<1, SILU, true>(a, c, nblocks, s) : dispatch_stream_xs<1, SILU>(a, c, nblocks, s);
+        case 2: return xf ? dispatch_stream_xs<2, SILU, true>(a, c, nblocks, s) : dispatch_stream_xs<2, SILU>(a, c, nblocks, s);
+        case 3: return xf ? dispatch_stream_xs<3, SILU, true>(a, c, nblocks, s) : dispatch_stream_xs<3, SILU>(a, c, nblocks, s);
+        case 4: return xf ? dispatch_stream_xs<4, SILU, true>(a, c, nblocks, s) : dispatch_stream_xs<4, SILU>(a, c, nblocks, s);
     }
     return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
 }
@@ -885,8 +886,15 @@ struct NormSpec {
     int64_t ldxo;
 };
 
+// A normed call whose projection runs on the stream kernel in one launch
+// gets its normalised rows in that kernel's fragment order.
+inline bool frag_prologue(int M, const krk_gemm_config& c) {
+    return c.kernel == KRK_KERNEL_STREAM && M <= kMaxRowsPerLaunch;
+}
+
 // Workspace of a call: [split-K counters and partials][normalised rows
-// M x K bf16 when a separate prologue writes them].
+// when a separate prologue writes them: M x K bf16, or in the stream
+// kernel's fragment order, 16·m_tiles rows x whole 512-k stages].
 struct WorkspaceLayout {
     size_t gemm;   // split-K part, at offset 0
     size_t n_off;  // offset of the normalised rows (0 if none)
@@ -896,8 +904,9 @@ WorkspaceLayout workspace_layout(int M, int N, int K, int epilogue, const krk_ge
     WorkspaceLayout l;
     l.gemm = workspace_for(M, N, epilogue, c);
     const bool prologue = normed && !norm_fused(M, N, K, epilogue, c);
+    const size_t nbytes = frag_prologue(M, c) ? krk::stream_frag_bytes(c.m_tiles, K) : (size_t)M * K * sizeof(uint16_t);
     l.n_off = prologue ? align_up(l.gemm, 256) : 0;
-    l.total = prologue ? l.n_off + (size_t)M * K * sizeof(uint16_t) : l.gemm;
+    l.total = prologue ? l.n_off + nbytes : l.gemm;
     return l;
 }
 
@@ -984,7 +993,17 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
     // writes into the workspace.
     const uint16_t* xin = static_cast<const uint16_t*>(x);
     int64_t ldin = ldx;
-    if (ns && !fused) {
+    const bool xf = ns && !fused && frag_prologue(M, c);
+    if (xf) {
+        unsigned char* nf = static_cast<unsigned char*>(workspace) + wl.n_off;
+        int mt = c.m_tiles;
+        void* args[] = {(void*)&x, (void*)&ldx, (void*)&na, (void*)&nf, (void*)&M, (void*)&K, (void*)&mt};
+        hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&krk::add_rmsnorm_frag_kernel), dim3(16 * mt),
+                                       dim3(krk::kNormThreads), args, 0, st);
+        if ((rc = hip_status(e, "add_rmsnorm_frag_kernel launch"))) return rc;
+        xin = reinterpret_cast<const uint16_t*>(nf);
+        ldin = 0;  // unused: the fragment order has no row stride
+    } else if (ns && !fused) {
         uint16_t* nrows = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + wl.n_off);
         int64_t ldn = K;
         void* args[] = {(void*)&x, (void*)&ldx, (void*)&na, (void*)&nrows, (void*)&ldn, (void*)&K};
@@ -1025,7 +1044,7 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
         } else if (c.kernel == KRK_KERNEL_MFMA_LDS) {
             rc = silu ? dispatch_mfma_lds<true>(a, c, g.nblocks, st) : dispatch_mfma_lds<false>(a, c, g.nblocks, st);
         } else if (c.kernel == KRK_KERNEL_STREAM) {
-            rc = silu ? dispatch_stream<true>(a, c, g.nblocks, st) : dispatch_stream<false>(a, c, g.nblocks, st);
+            rc = silu ? dispatch_stream<true>(a, c, g.nblocks, st, xf) : dispatch_stream<false>(a, c, g.nblocks, st, xf);
         } else {
             rc = silu ? dispatch_valu<true>(a, c, g.nblocks, st) : dispatch_valu<false>(a, c, g.nblocks, st);
         }

@@ -340,19 +340,35 @@ def test_normed_fused_plans(lib):
     assert lib.krk_gemm_normed_plan(1, 6144, 2560, NONE, None) == _lib.KRK_ERR_INVALID
 
 
+def _normed_rows_bytes(lib, M, N, K, epi, cfg=None):
+    """Bytes of the normalised rows a prologue kernel writes: M x K bf16, or,
+    in front of a stream-kernel launch (M <= 64), the kernel's fragment order
+    over 16 * m_tiles rows and whole 512-k stages."""
+    c = GemmConfig()
+    assert lib.krk_gemm_resolve(M, N, K, epi, ctypes.byref(cfg) if cfg is not None else None, ctypes.byref(c)) == 0
+    if c.kernel == _lib.KERNEL_STREAM and M <= 64:
+        return 16 * c.m_tiles * -(-K // 512) * 512 * 2
+    return M * K * 2
+
+
 def test_normed_workspace_layouts(lib):
-    """Prologue-kernel plans add the M normalised rows after the split-K area;
-    fused plans add nothing."""
-    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["qkv"], 100), (QWEN["gate_up"], 64), (QWEN["lm_head"], 64)]:
+    """Prologue-kernel plans add the normalised rows after the split-K area
+    (in the stream kernel's fragment order in front of that kernel); fused
+    plans add nothing."""
+    for (N, K, epi), M in [(QWEN["qkv"], 32), (QWEN["qkv"], 100), (QWEN["gate_up"], 64), (QWEN["lm_head"], 64),
+                           (QWEN["gate_up"], 20), (QWEN["lm_head"], 100)]:
         assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == 0
         plain = lib.krk_gemm_workspace_bytes(M, N, K, epi)
         normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, None)
-        assert normed == -(-plain // 256) * 256 + M * K * 2
+        assert normed == -(-plain // 256) * 256 + _normed_rows_bytes(lib, M, N, K, epi), (N, M)
+    assert _normed_rows_bytes(lib, 20, *QWEN["gate_up"]) == 32 * 2560 * 2  # two 16-row tiles
+    assert _normed_rows_bytes(lib, 100, *QWEN["lm_head"]) == 100 * 2560 * 2  # two launches: rows
     sep = GemmConfig(kernel=_lib.KERNEL_STREAM, prologue=1)
-    for (N, K, epi), M in [(QWEN["gate_up"], 16), (QWEN["lm_head"], 17)]:
+    for (N, K, epi), M in [(QWEN["gate_up"], 16), (QWEN["lm_head"], 17), ((2 * 96, 1000, SILU), 17)]:
         plain = lib.krk_gemm_config_workspace_bytes(M, N, K, epi, ctypes.byref(sep))
         normed = lib.krk_gemm_normed_workspace_bytes(M, N, K, epi, ctypes.byref(sep))
-        assert normed == -(-plain // 256) * 256 + M * K * 2, (N, M)
+        assert normed == -(-plain // 256) * 256 + _normed_rows_bytes(lib, M, N, K, epi, sep), (N, M)
+    assert _normed_rows_bytes(lib, 17, 192, 1000, SILU, sep) == 32 * 1024 * 2  # ragged K: whole stages
     for (N, K, epi), M in [(QWEN["qkv"], 1), (QWEN["gate_up"], 2), (QWEN["lm_head"], 1)]:
         assert lib.krk_gemm_normed_fused(M, N, K, epi, None) == 1
         cfg = GemmConfig()

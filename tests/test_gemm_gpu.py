@@ -916,6 +916,29 @@ def test_normed_fused_plans_and_separate_prologue(device, shape, M):
     _check_normed(x, y, wn, w, epi, xo2, out2, f"normed prologue kernel {shape} M={M}")
 
 
+@pytest.mark.parametrize("M,N,K,epi,splits", [
+    (5, 600, 2560, NONE, 1), (16, 2 * 300, 2560, SILU, 1), (17, 1000, 1000, NONE, 1), (20, 2 * 200, 2056, SILU, 1),
+    (32, 2 * 600, 2560, SILU, 1), (33, 520, 2560, NONE, 1), (48, 2 * 96, 1032, SILU, 1), (64, 1000, 2560, NONE, 1),
+    (20, 600, 2560, NONE, 2), (40, 2 * 300, 5120, SILU, 2), (64, 520, 4096, NONE, 3), (100, 600, 2560, NONE, 1)])
+def test_normed_stream_fragment_order(device, M, N, K, epi, splits):
+    """Normed calls on the stream kernel, whose prologue writes the
+    normalised rows in the kernel's MFMA fragment order (rows past M and k
+    past K up to whole 512-k stages zero): one to four 16-row tiles, ragged
+    K (down to an 8-element last stage) and N, split K, two ring depths, and
+    past 64 rows the row-major path.  xout bit-exact, outputs against the
+    oracle, and a second call with other inputs on the same workspace (which
+    the first left holding the previous rows)."""
+    w = R.randn_bf16((N, K), 9510 + N, 0.02)
+    for depth in (3, 5):
+        cfg = dict(kernel=_lib.KERNEL_STREAM, splits=splits, unroll=depth)
+        ws = None
+        for rep in range(2):
+            x, y, wn = _norm_inputs(M, K, 9500 + M + 10 * rep)
+            say("normed stream", M, N, K, epi, cfg, rep)
+            xo, out, ws = krk_normed(x, y, wn, w, epi, cfg, ws=ws, with_ws=True)
+            _check_normed(x, y, wn, w, epi, xo, out, f"normed stream {cfg} M={M} call {rep}")
+
+
 def _normed_fused_configs(M, epi):
     """VALU configurations at the fused depth (M <= 8): every W-rows-per-wave
     and wave count (those with fewer waves than 512-k blocks do not fuse);
