@@ -63,17 +63,7 @@ __host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth, int nre
 // blocks, [slot][16·MT rows][CB channels].
 __host__ __device__ constexpr size_t stream_out_bytes(int MT, bool silu) { return (size_t)(silu ? 8 : 16) * 16 * MT * 2; }
 
-// Byte offset of MFMA fragment (st, ks, i) of lane `lane` in x held in
-// fragment order: 512-k stage st, 32-k step ks of that stage, 16-row tile i
-// of MT; the 64 lanes' 16-byte pieces of one fragment are one contiguous
-// 1 KB run (lane (r, q) = x[16i + r][512·st + 32·ks + 8q .. +7]).
-__host__ __device__ constexpr size_t stream_frag_offset(int st, int ks, int i, int lane, int MT) {
-    return ((((size_t)st * (kStreamKC / 32) + ks) * MT + i) * 64 + lane) * 16;
-}
-// Bytes of x in fragment order: 16·MT rows x whole 512-k stages.
-__host__ __device__ constexpr size_t stream_frag_bytes(int MT, int K) {
-    return (size_t)MT * 16 * ((K + kStreamKC - 1) / kStreamKC) * kStreamKC * 2;
-}
+static_assert(kStreamKC == kFragKC, "fragment order is laid out in the stream kernel's stages");
 
 // MT: 16-row m tiles (M <= 16·MT).  XS: most K stages a workgroup owns (its
 // x fragments live in X[XS][2][MT]).  SILU: gate/up blocks with the epilogue.
@@ -81,7 +71,7 @@ __host__ __device__ constexpr size_t stream_frag_bytes(int MT, int K) {
 // largest (value, index) keys over its blocks (krk_select.h) and writes them
 // to sa.keys[m][workgroup * SK ...]; y (the logits) is written only when
 // non-null.  0: no selection.
-// XF: x is given in fragment order (stream_frag_offset; rows past M and k
+// XF: x is given in fragment order (frag_offset; rows past M and k
 // past K hold zeros), as add_rmsnorm_frag_kernel writes the normalised rows
 // of a normed call: every fragment is one contiguous 1 KB load, and the trip
 // of x through LDS is skipped.
@@ -166,7 +156,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
                     const u32x4 v = *reinterpret_cast<const u32x4*>(
-                        xf + stream_frag_offset(st, KPW * wave + kk, i, lane, MT));
+                        xf + frag_offset(st, KPW * wave + kk, i, lane, MT));
                     X[j][kk][i] = j < nst ? v : u32x4{0u, 0u, 0u, 0u};
                 }
         }
@@ -390,66 +380,6 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                     store_agent_u64(sa.keys + (int64_t)m * sa.ldk + (int64_t)blockIdx.x * KL + q2, best[j][q2]);
             }
         }
-    }
-}
-
-// The stand-alone residual-add + RMSNorm prologue (add_rmsnorm_kernel's
-// arithmetic and rounding points) writing the normalised rows in the stream
-// kernel's fragment order for MT tiles (stream_frag_offset), so that a normed
-// call's stream kernel loads x as whole 1 KB runs and skips its trip through
-// LDS.  Workgroup m of 16·MT writes row m: for m < M the normalised row (and
-// xout[m]) plus zeros for k from K up to whole 512-k stages; rows past M are
-// zeros.
-__global__ void __launch_bounds__(kNormThreads)
-add_rmsnorm_frag_kernel(const uint16_t* __restrict__ x, int64_t ldx, NormArgs a, unsigned char* __restrict__ nf,
-                        int M, int K, int MT) {
-    __shared__ float red[kNormThreads / 64];
-    const int m = blockIdx.x;
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int KP = (K + kStreamKC - 1) / kStreamKC * kStreamKC;
-    const int i = m >> 4;
-    const int r = m & 15;
-    const u32x4 zero{0u, 0u, 0u, 0u};
-    auto put = [&](int k, const u32x4& v) {
-        const int st = k / kStreamKC;
-        const int ks = (k % kStreamKC) / 32;
-        const int q = (k % 32) / 8;
-        *reinterpret_cast<u32x4*>(nf + stream_frag_offset(st, ks, i, r + 16 * q, MT)) = v;
-    };
-    if (m >= M) {  // the whole workgroup: a padding row
-        for (int k = 8 * t; k < KP; k += 8 * kNormThreads) put(k, zero);
-        return;
-    }
-    const uint16_t* xr = x + (int64_t)m * ldx;
-    const uint16_t* dr = a.d + (int64_t)m * a.ldd;
-    uint16_t* xo = a.xout + (int64_t)m * a.ldxo;
-    u32x4 s[kNormMaxVec], g[kNormMaxVec];
-    float ss = 0.0f;
-#pragma unroll
-    for (int v = 0; v < kNormMaxVec; ++v) {
-        const int k = 8 * (t + kNormThreads * v);
-        if (k < K) {
-            s[v] = add_bf16x8(*reinterpret_cast<const u32x4*>(xr + k), *reinterpret_cast<const u32x4*>(dr + k));
-            g[v] = *reinterpret_cast<const u32x4*>(a.wn + k);
-            *reinterpret_cast<u32x4*>(xo + k) = s[v];
-            ss = sumsq_bf16x8(s[v], ss);
-        }
-    }
-    for (int k = K + 8 * t; k < KP; k += 8 * kNormThreads) put(k, zero);
-    // Fixed-order reduction, as add_rmsnorm_kernel.
-    wave_fold<1, 32>(&ss, lane);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float tot = red[0];
-#pragma unroll
-    for (int wv = 1; wv < kNormThreads / 64; ++wv) tot += red[wv];
-    const float rstd = rms_rstd(tot, K, a.eps);
-#pragma unroll
-    for (int v = 0; v < kNormMaxVec; ++v) {
-        const int k = 8 * (t + kNormThreads * v);
-        if (k < K) put(k, normalize_bf16x8(s[v], rstd, g[v]));
     }
 }
 
