@@ -134,7 +134,7 @@ typedef struct krk_gemm_config {
     int x_preload; /* MFMA_LDS: 1 = x rows loaded with every stage's weight
                      rows; 2 = x rows of the whole K loaded into registers
                      once, before the first stage, so the stage loop loads
-                     weights only (k_chunk 512, K unsplit, K <= 2560,
+                     weights only (k_chunk 512, K unsplit, K <= 4096,
                      m_tiles <= 2, no token selection); 0 = the dispatcher's
                      choice (the plan's when the plan uses this kernel, else
                      1).  Other kernels: ignored. */

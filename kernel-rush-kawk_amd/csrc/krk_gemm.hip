@@ -119,9 +119,12 @@ const TableEntry kTable[] = {
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 8, 5, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 3, 6, kcfg(KRK_KERNEL_VALU, 1, 4, 5, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 7, 8, kcfg(KRK_KERNEL_VALU, 2, 4, 8, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512)},
-    // 3 stages in flight up to three x tiles, 2 with four (1-5% faster each way)
-    {2560, 4096, KRK_EPILOGUE_NONE, 17, 48, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
+    // M = 9-32: K unsplit on 160 blocks of 16 channels with x held in
+    // registers for all 8 stages (4-11% faster than staging x with every
+    // stage, and than 3 K splits at M = 17-32); above, 3 stages in flight up
+    // to three x tiles, 2 with four (1-5% faster each way)
+    {2560, 4096, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512, 16, 2)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 33, 48, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 4096, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3, 256)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
@@ -279,10 +282,10 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
 constexpr int kLdsPf3MaxTiles = 6;
 constexpr bool mfma_lds_pf3(int MT, int NT) { return MT + NT <= kLdsPf3MaxTiles; }
 // MFMA_LDS with x held in registers for the whole K (x_preload = 2): 512-k
-// stages, K unsplit in at most kLdsNormStages of them, up to two x tiles.
+// stages, K unsplit in at most kLdsXpreStages of them, up to two x tiles.
 constexpr int kLdsXpreMaxMTiles = 2;
 inline bool lds_xpre_ok(const krk_gemm_config& c, int K) {
-    return c.k_chunk == 512 && c.splits == 1 && cdiv(K, 512) <= krk::kLdsNormStages && c.m_tiles <= kLdsXpreMaxMTiles;
+    return c.k_chunk == 512 && c.splits == 1 && cdiv(K, 512) <= krk::kLdsXpreStages && c.m_tiles <= kLdsXpreMaxMTiles;
 }
 
 // Dynamic LDS a gfx950 workgroup may use: 160 KB less room for the kernels'
@@ -387,7 +390,7 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
             return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=%d not in {1, 2}", c.x_preload);
         if (c.x_preload == 2 && !lds_xpre_ok(c, K))
             return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=2 needs k_chunk 512, splits 1, K <= %d and m_tiles <= %d",
-                        krk::kLdsNormStages * 512, kLdsXpreMaxMTiles);
+                        krk::kLdsXpreStages * 512, kLdsXpreMaxMTiles);
         *out = c;
         return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_STREAM) {
@@ -535,7 +538,7 @@ int dispatch_mfma(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hi
     return fail(KRK_ERR_UNSUPPORTED, "MFMA m_tiles=%d", c.m_tiles);
 }
 
-template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false, bool XPRE = false>
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false, int XPRE = 0>
 int launch_mfma_lds(const LaunchArgs& a, int nblocks, hipStream_t stream, krk::SelectArgs sa = {},
                     krk::NormArgs na = {}) {
     if constexpr ((PF == 3 && !mfma_lds_pf3(MT, NT)) || !krk::mfma_lds_kc_ok(MT, NT, KC)) {
@@ -567,8 +570,13 @@ int dispatch_mfma_lds_pf(const LaunchArgs& a, const krk_gemm_config& c, int nblo
 template <int MT, int NT, bool SILU>
 int dispatch_mfma_lds_xpre(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
     if constexpr (MT <= kLdsXpreMaxMTiles && krk::mfma_lds_kc_ok(MT, NT, 512)) {
-        if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, false, true>(a, nblocks, s);
-        return launch_mfma_lds<MT, NT, 2, 512, SILU, false, false, true>(a, nblocks, s);
+        // The loop runs all of the held stages: 5 where K fits them, else 8.
+        if (cdiv(a.K, 512) <= krk::kLdsNormStages) {
+            if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, false, krk::kLdsNormStages>(a, nblocks, s);
+            return launch_mfma_lds<MT, NT, 2, 512, SILU, false, false, krk::kLdsNormStages>(a, nblocks, s);
+        }
+        if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 512, SILU, false, false, krk::kLdsXpreStages>(a, nblocks, s);
+        return launch_mfma_lds<MT, NT, 2, 512, SILU, false, false, krk::kLdsXpreStages>(a, nblocks, s);
     } else {
         return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=2 with %d x %d tiles", MT, NT);
     }

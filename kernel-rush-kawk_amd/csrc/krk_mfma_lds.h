@@ -45,6 +45,9 @@ constexpr int kLdsWaves = 8;
 // Stages of 512 k the fused RMSNorm prologue holds in registers: K <= 2560,
 // the hidden size every normed projection reads.
 constexpr int kLdsNormStages = 5;
+// Most 512-k stages of x the XPRE variants hold in registers (o_proj's
+// K = 4096 with one or two x tiles); shorter K uses kLdsNormStages.
+constexpr int kLdsXpreStages = 8;
 
 // k per stage: 512 fits two tiles of NR + MX rows in LDS up to four 16-row
 // tiles (128 KB); 256 halves the footprint (more workgroups per CU when the
@@ -71,15 +74,15 @@ __host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool
 // keeps the normalised rows in registers, from which every stage's x rows
 // are staged; no x loads remain in the loop.  Workgroup 0 writes s to
 // na.xout after the loop.
-// XPRE: the same register-held x rows without the prologue: x for the whole
-// K (at most kLdsNormStages 512-k stages, K unsplit) is loaded once before
-// the first stage, and the stage loop loads weights only.
+// XPRE (> 0): the same register-held x rows without the prologue: x for the
+// whole K (at most XPRE 512-k stages, K unsplit) is loaded once before the
+// first stage, and the stage loop loads weights only.
 // cb: output channels per block (a multiple of 8, at most 16·NH).  Below
 // 16·NH the last tile is partly padding: its rows past cb are not loaded
 // (zeros in the tile) and their outputs not stored.  This lets a shape use
 // all 256 CUs with whole K (qkv: 6144 = 256 x 24 channels) instead of
 // leaving CUs idle or splitting K.
-template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false, bool XPRE = false>
+template <int MT, int NT, int PF, int KC, bool SILU, bool SEL = false, bool NORM = false, int XPRE = 0>
 __global__ void __launch_bounds__(64 * kLdsWaves)
 mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const uint16_t* __restrict__ w, int64_t ldw,
@@ -89,6 +92,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     static_assert(!(SEL && SILU), "selection reads plain logits");
     static_assert(!(NORM || XPRE) || (KC == 512 && !SEL), "x rows held in registers are whole 512-k rows");
     static_assert(!(NORM && XPRE), "the fused prologue already holds x in registers");
+    static_assert(XPRE == 0 || XPRE == kLdsNormStages || XPRE == kLdsXpreStages, "instantiated x-register depths");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     static_assert(!SILU || (NT % 2 == 0), "SILU pairs gate and up tiles");
     static_assert(PF >= 2, "at least two stages in flight");
@@ -202,7 +206,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         // K unsplit (sb = 0) in nst <= XN stages of 512: lane l of wave w
         // holds k = 512·b + 8l of rows w + 8j for every stage b.  Rows past
         // M and k past K are zero.
-        constexpr int XN = kLdsNormStages;
+        constexpr int XN = NORM ? kLdsNormStages : XPRE;
         const int nst = KST;
         u32x4 xr[XN][LX], dr[XN][LX], gv[XN];
         u32x4 sv[XN][LX];

@@ -147,7 +147,7 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
 
 def test_x_preload_resolution(lib):
     """x_preload resolves to the plan's choice for MFMA_LDS (2 for qkv at
-    M = 9-32, 1 at 33-64 and where x cannot be held), to 0 for the other
+    M = 5-32 and o at M = 9-32, 1 at 33-64 and where x cannot be held), to 0 for the other
     kernels, and a caller's 1 or 2 is kept where it is valid."""
     def resolve(M, N, K, **kw):
         out = GemmConfig()
@@ -160,7 +160,12 @@ def test_x_preload_resolution(lib):
     assert resolve(12, 6144, 2560, kernel=3, k_chunk=256)["x_preload"] == 1  # the plan's 2 does not apply
     assert resolve(12, 6144, 2560, kernel=3, x_preload=1)["x_preload"] == 1
     assert resolve(24, 6144, 2560, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2
-    assert resolve(40, 2560, 4096, kernel=3)["x_preload"] == 1  # o: 8 stages of 512
+    assert resolve(20, 2560, 4096)["x_preload"] == 2  # o: 8 stages of 512 in registers
+    assert resolve(40, 2560, 4096, kernel=3)["x_preload"] == 1  # three x tiles: staged with every stage
+    for K, ok in ((4096, True), (4104, False)):  # at most 8 stages of 512
+        want = GemmConfig.from_dict(dict(kernel=3, n_tiles=1, k_chunk=512, x_preload=2))
+        rc = lib.krk_gemm_resolve(20, 2560, K, NONE, ctypes.byref(want), ctypes.byref(GemmConfig()))
+        assert (rc == 0) == ok, (K, _lib.last_error())
     for kernel in (1, 2, 5):
         assert resolve(8, 6144, 2560, kernel=kernel, x_preload=2)["x_preload"] == 0
 
