@@ -134,9 +134,8 @@ typedef struct krk_gemm_config {
     int x_preload; /* MFMA_LDS: 1 = x rows loaded with every stage's weight
                      rows; 2 = x rows of the whole K loaded into registers
                      once, before the first stage, so the stage loop loads
-                     weights only (K unsplit, no token selection; k_chunk
-                     512 with K <= 4096 and m_tiles <= 2, or k_chunk 256
-                     with K <= 2560 and n_tiles <= 2); 0 = the dispatcher's
+                     weights only (k_chunk 512, K unsplit, K <= 4096,
+                     m_tiles <= 2, no token selection); 0 = the dispatcher's
                      choice (the plan's when the plan uses this kernel, else
                      1).  Other kernels: ignored. */
 } krk_gemm_config;

@@ -281,15 +281,11 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
 // 256 VGPRs without spilling up to this many 16-row tiles (m + n).
 constexpr int kLdsPf3MaxTiles = 6;
 constexpr bool mfma_lds_pf3(int MT, int NT) { return MT + NT <= kLdsPf3MaxTiles; }
-// MFMA_LDS with x held in registers for the whole K (x_preload = 2), K
-// unsplit: 512-k stages, at most kLdsXpreStages of them, up to two x tiles;
-// or 256-k stages, at most kLdsXpre256Stages, up to two weight tiles.
+// MFMA_LDS with x held in registers for the whole K (x_preload = 2): 512-k
+// stages, K unsplit in at most kLdsXpreStages of them, up to two x tiles.
 constexpr int kLdsXpreMaxMTiles = 2;
-constexpr int kLdsXpre256MaxNTiles = 2;
 inline bool lds_xpre_ok(const krk_gemm_config& c, int K) {
-    if (c.splits != 1) return false;
-    if (c.k_chunk == 512) return cdiv(K, 512) <= krk::kLdsXpreStages && c.m_tiles <= kLdsXpreMaxMTiles;
-    return c.k_chunk == 256 && cdiv(K, 256) <= krk::kLdsXpre256Stages && c.n_tiles <= kLdsXpre256MaxNTiles;
+    return c.k_chunk == 512 && c.splits == 1 && cdiv(K, 512) <= krk::kLdsXpreStages && c.m_tiles <= kLdsXpreMaxMTiles;
 }
 
 // Dynamic LDS a gfx950 workgroup may use: 160 KB less room for the kernels'
@@ -393,11 +389,8 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
         if (c.x_preload != 1 && c.x_preload != 2)
             return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=%d not in {1, 2}", c.x_preload);
         if (c.x_preload == 2 && !lds_xpre_ok(c, K))
-            return fail(KRK_ERR_UNSUPPORTED,
-                        "MFMA_LDS x_preload=2 needs splits 1 and k_chunk 512 with K <= %d and m_tiles <= %d, or "
-                        "k_chunk 256 with K <= %d and n_tiles <= %d",
-                        krk::kLdsXpreStages * 512, kLdsXpreMaxMTiles, krk::kLdsXpre256Stages * 256,
-                        kLdsXpre256MaxNTiles);
+            return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=2 needs k_chunk 512, splits 1, K <= %d and m_tiles <= %d",
+                        krk::kLdsXpreStages * 512, kLdsXpreMaxMTiles);
         *out = c;
         return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_STREAM) {
@@ -589,25 +582,12 @@ int dispatch_mfma_lds_xpre(const LaunchArgs& a, const krk_gemm_config& c, int nb
     }
 }
 
-// x held in registers in 256-k stages (x_preload = 2, k_chunk 256).
-template <int MT, int NT, bool SILU>
-int dispatch_mfma_lds_xpre256(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
-    if constexpr (NT <= kLdsXpre256MaxNTiles) {
-        constexpr int XN = krk::kLdsXpre256Stages;
-        if (c.unroll == 3) return launch_mfma_lds<MT, NT, 3, 256, SILU, false, false, XN>(a, nblocks, s);
-        return launch_mfma_lds<MT, NT, 2, 256, SILU, false, false, XN>(a, nblocks, s);
-    } else {
-        return fail(KRK_ERR_UNSUPPORTED, "MFMA_LDS x_preload=2 with 256-k stages and %d weight tiles", NT);
-    }
-}
-
 template <int MT, int NT, bool SILU>
 int dispatch_mfma_lds_kc(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
     if (c.k_chunk == 512) {
         if (c.x_preload == 2) return dispatch_mfma_lds_xpre<MT, NT, SILU>(a, c, nblocks, s);
         return dispatch_mfma_lds_pf<MT, NT, 512, SILU>(a, c, nblocks, s);
     }
-    if (c.x_preload == 2) return dispatch_mfma_lds_xpre256<MT, NT, SILU>(a, c, nblocks, s);
     return dispatch_mfma_lds_pf<MT, NT, 256, SILU>(a, c, nblocks, s);
 }
 
@@ -1589,11 +1569,10 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
                 for (int sp : wide_splits)
                     for (int ch : chans)
                         if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, sp, kc, 0, ch, 1});
-        // x held in registers for the whole K (one K split).
+        // x held in registers for the whole K (one K split, 512-k stages).
         for (int pf : {2, 3})
-            for (int kc : {256, 512})
-                for (int ch : chans)
-                    if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, 1, kc, 0, ch, 2});
+            for (int ch : chans)
+                if (ch >= 8) add(krk_gemm_config{KRK_KERNEL_MFMA_LDS, 0, nt, pf, 0, 1, 512, 0, ch, 2});
     }
     for (int d = 2; d <= krk::kStreamMaxDepth; ++d)
         for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});

@@ -48,8 +48,6 @@ constexpr int kLdsNormStages = 5;
 // Most 512-k stages of x the XPRE variants hold in registers (o_proj's
 // K = 4096 with one or two x tiles); shorter K uses kLdsNormStages.
 constexpr int kLdsXpreStages = 8;
-// With 256-k stages (three or four x tiles), K <= 2560.
-constexpr int kLdsXpre256Stages = 10;
 
 // k per stage: 512 fits two tiles of NR + MX rows in LDS up to four 16-row
 // tiles (128 KB); 256 halves the footprint (more workgroups per CU when the
@@ -77,7 +75,7 @@ __host__ __device__ constexpr size_t mfma_lds_bytes(int MT, int NT, int KC, bool
 // are staged; no x loads remain in the loop.  Workgroup 0 writes s to
 // na.xout after the loop.
 // XPRE (> 0): the same register-held x rows without the prologue: x for the
-// whole K (at most XPRE stages of KC, K unsplit) is loaded once before the
+// whole K (at most XPRE 512-k stages, K unsplit) is loaded once before the
 // first stage, and the stage loop loads weights only.
 // cb: output channels per block (a multiple of 8, at most 16·NH).  Below
 // 16·NH the last tile is partly padding: its rows past cb are not loaded
@@ -92,12 +90,9 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 int M, int N, int K, int splits, int cb,
                 float* __restrict__ part, uint32_t* __restrict__ ctr, SelectArgs sa, NormArgs na) {
     static_assert(!(SEL && SILU), "selection reads plain logits");
-    static_assert(!(NORM || XPRE) || !SEL, "x rows held in registers serve plain and normed calls");
-    static_assert(!NORM || KC == 512, "the fused prologue holds whole 512-k rows");
+    static_assert(!(NORM || XPRE) || (KC == 512 && !SEL), "x rows held in registers are whole 512-k rows");
     static_assert(!(NORM && XPRE), "the fused prologue already holds x in registers");
-    static_assert(XPRE == 0 || (KC == 512 && (XPRE == kLdsNormStages || XPRE == kLdsXpreStages)) ||
-                      (KC == 256 && XPRE == kLdsXpre256Stages),
-                  "instantiated x-register depths");
+    static_assert(XPRE == 0 || XPRE == kLdsNormStages || XPRE == kLdsXpreStages, "instantiated x-register depths");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     static_assert(!SILU || (NT % 2 == 0), "SILU pairs gate and up tiles");
     static_assert(PF >= 2, "at least two stages in flight");
@@ -208,13 +203,10 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     };
 
     if constexpr (NORM || XPRE) {
-        // K unsplit (sb = 0) in nst <= XN stages of KC: wave w holds the x
-        // rows it stages (xrow(j): w + 8j with 512-k stages; with 256-k
-        // stages two rows per load, lanes 32-63 on the second) of every
-        // stage b, lane l at k = KC·b + 8·(l mod KC/8).  Rows past M and k
-        // past K are zero.
+        // K unsplit (sb = 0) in nst <= XN stages of 512: lane l of wave w
+        // holds k = 512·b + 8l of rows w + 8j for every stage b.  Rows past
+        // M and k past K are zero.
         constexpr int XN = NORM ? kLdsNormStages : XPRE;
-        auto xrow = [&](int j) { return RPL * (wave + WV * j) + lrow; };
         const int nst = KST;
         u32x4 xr[XN][LX], dr[XN][LX], gv[XN];
         u32x4 sv[XN][LX];
@@ -225,7 +217,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             if constexpr (NORM) gv[b] = load_cached16(na.wn + kc);
 #pragma unroll
             for (int j = 0; j < LX; ++j) {
-                const int m = xrow(j);
+                const int m = wave + WV * j;
                 const int mm = m < M ? m : M - 1;
                 xr[b][j] = load_cached16(x + (int64_t)mm * ldx + kc);
                 if constexpr (NORM) dr[b][j] = load_cached16(na.d + (int64_t)mm * na.ldd + kc);
@@ -246,7 +238,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             const uint32_t mk = (in && st * KC + 8 * lsub < K) ? 0xffffffffu : 0u;
 #pragma unroll
             for (int j = 0; j < LPW; ++j) {
-                const int tr = j < LW ? RPL * (wave + WV * j) + lrow : NR + xrow(j - LW);
+                const int tr = j < LW ? wave + WV * j : NR + wave + WV * (j - LW);
                 u32x4 v = j < LW ? Rw[j] : Xr[j - LW];
                 if (j < LW && !rowok[j]) v = u32x4{0u, 0u, 0u, 0u};
                 if (!in || rag) v &= mk;
@@ -298,7 +290,7 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             for (int b = 0; b < XN; ++b)
 #pragma unroll
                 for (int j = 0; j < LX; ++j) {
-                    const bool live = b < nst && xrow(j) < M;
+                    const bool live = b < nst && wave + WV * j < M;
                     xr[b][j] = live ? xr[b][j] : u32x4{0u, 0u, 0u, 0u};
                 }
         }

@@ -157,8 +157,7 @@ def test_x_preload_resolution(lib):
     assert resolve(20, 6144, 2560)["x_preload"] == 2
     assert resolve(32, 6144, 2560)["x_preload"] == 2
     assert resolve(33, 6144, 2560)["x_preload"] == 1
-    assert resolve(12, 6144, 2560, kernel=3, k_chunk=256)["x_preload"] == 2  # the plan's 2, in 256-k stages
-    assert resolve(12, 6144, 2560, kernel=3, k_chunk=256, n_tiles=4)["x_preload"] == 1  # the plan's 2 does not apply
+    assert resolve(12, 6144, 2560, kernel=3, k_chunk=256)["x_preload"] == 1  # the plan's 2 does not apply
     assert resolve(12, 6144, 2560, kernel=3, x_preload=1)["x_preload"] == 1
     assert resolve(24, 6144, 2560, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2
     assert resolve(20, 2560, 4096)["x_preload"] == 2  # o: 8 stages of 512 in registers
@@ -167,10 +166,6 @@ def test_x_preload_resolution(lib):
         want = GemmConfig.from_dict(dict(kernel=3, n_tiles=1, k_chunk=512, x_preload=2))
         rc = lib.krk_gemm_resolve(20, 2560, K, NONE, ctypes.byref(want), ctypes.byref(GemmConfig()))
         assert (rc == 0) == ok, (K, _lib.last_error())
-    # 256-k stages: three or four x tiles, at most ten stages (K <= 2560).
-    assert resolve(48, 6144, 2560, kernel=3, n_tiles=2, k_chunk=256, x_preload=2)["x_preload"] == 2
-    want = GemmConfig.from_dict(dict(kernel=3, n_tiles=2, k_chunk=256, x_preload=2))
-    assert lib.krk_gemm_resolve(48, 6144, 2568, NONE, ctypes.byref(want), ctypes.byref(GemmConfig())) < 0
     for kernel in (1, 2, 5):
         assert resolve(8, 6144, 2560, kernel=kernel, x_preload=2)["x_preload"] == 0
 
@@ -189,10 +184,9 @@ def test_x_preload_resolution(lib):
     (dict(kernel=3, m_tiles=2, n_tiles=4, k_chunk=512), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
     (dict(kernel=3, k_chunk=384), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
     (dict(kernel=3, x_preload=3), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
-    (dict(kernel=3, k_chunk=256, n_tiles=4, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
+    (dict(kernel=3, k_chunk=256, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
     (dict(kernel=3, k_chunk=512, n_tiles=2, splits=2, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
     (dict(kernel=3, m_tiles=3, n_tiles=1, k_chunk=512, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
-    (dict(kernel=3, m_tiles=3, n_tiles=4, unroll=2, k_chunk=256, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
 ])
 def test_config_errors(lib, cfg, code, msg):
     c = GemmConfig.from_dict(cfg)

@@ -72,3 +72,22 @@ def test_valu_dma_waits_cover_only_the_dmas(disassembly):
         assert wait <= loads, f"{name}: waits for vmcnt({wait}) with only {loads} loads issued after the last DMA"
         checked += 1
     assert checked >= 10, checked
+
+
+def test_lds_x_in_registers_keeps_weight_stages_in_flight(disassembly):
+    """The LDS-staged kernel's register-held-x variants (XPRE, the last
+    template argument > 0) load x for the whole K, then the first weight
+    stages, and the first stage waits only for what it stashes.  A full
+    drain (vmcnt(0)) before the first barrier means the compiler sank an x
+    load under a condition and waits for every weight stage there (seen
+    once, 4-5% slower): no such wait may precede the first barrier."""
+    checked = 0
+    for name, body in _functions(disassembly):
+        m = re.search(r"mfma_lds_kernelILi\d+ELi\d+ELi\d+ELi(\d+)ELb[01]ELb0ELb0ELi(\d+)EE", name)
+        if not m or int(m.group(2)) == 0:
+            continue
+        first_barrier = next(i for i, l in enumerate(body) if l.startswith("s_barrier"))
+        drains = [l for l in body[:first_barrier] if re.match(r"s_waitcnt\s.*vmcnt\(0\)", l)]
+        assert not drains, f"{name}: {drains[0]} before the first barrier"
+        checked += 1
+    assert checked >= 16, checked

@@ -532,34 +532,6 @@ def _lds_xpre_configs(M, silu):
                        channels=ch, x_preload=2)
 
 
-def _lds_xpre256_configs(M, silu):
-    """LDS-staged configurations that hold x in registers in 256-k stages
-    (x_preload = 2, k_chunk 256): one to four x tiles, one or two weight
-    tiles, two or three stages in flight, all of the tiles' channels and 8
-    fewer."""
-    mt_min = -(-min(M, 64) // 16)
-    for mt, nt, pf in itertools.product(range(mt_min, 5), (1, 2), (2, 3)):
-        if silu and nt % 2:
-            continue
-        full = 16 * (nt // 2 if silu else nt)
-        for ch in sorted({full, max(8, full - 8)}):
-            yield dict(kernel=_lib.KERNEL_MFMA_LDS, m_tiles=mt, n_tiles=nt, unroll=pf, k_chunk=256, splits=1,
-                       channels=ch, x_preload=2)
-
-
-@pytest.mark.parametrize("M,N,K,epi", [(33, 6144, 2560, NONE), (48, 520, 2056, NONE), (64, 130, 512, NONE),
-                                       (40, 2 * 96, 2560, SILU), (64, 2 * 600, 1032, SILU), (17, 200, 1000, NONE),
-                                       (3, 96, 8, NONE), (64, 6144, 2560, NONE)])
-def test_lds_x_in_registers_256k_configs(device, M, N, K, epi):
-    """x held in registers in 256-k stages (ten stages, K up to 2560, run as
-    zeros past K; ragged K down to one 8-element chunk, ragged N, partial
-    channel blocks, one to four x tiles, both epilogues) gives the oracle's
-    results within the fp32 bound."""
-    x = R.randn_bf16((M, K), 8880 + M)
-    w = R.randn_bf16((N, K), 8881 + N, 0.02)
-    _run_configs(x, w, epi, _lds_xpre256_configs(M, epi == SILU))
-
-
 @pytest.mark.parametrize("M,N,K,epi", [(1, 96, 1536, NONE), (9, 200, 1000, NONE), (16, 6144, 2560, NONE),
                                        (24, 520, 2056, NONE), (32, 130, 512, NONE), (3, 96, 8, NONE),
                                        (13, 2 * 96, 2560, SILU), (20, 2 * 200, 1032, SILU), (32, 2 * 600, 2048, SILU),
