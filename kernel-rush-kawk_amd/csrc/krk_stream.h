@@ -160,7 +160,8 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                     X[j][kk][i] = j < nst ? v : u32x4{0u, 0u, 0u, 0u};
                 }
         }
-        // The ring starts once x has landed, as below.
+        // The ring starts once x has landed, as below (issuing it right
+        // behind these loads measured 0.3-0.5 us slower per call).
         vm_wait<0>();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         for (int d = 0; d < depth - 1 && d < T; ++d) issue(d);
