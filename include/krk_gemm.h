@@ -134,8 +134,9 @@ typedef struct krk_gemm_config {
     int x_preload; /* MFMA_LDS: 1 = x rows loaded with every stage's weight
                      rows; 2 = x rows of the whole K loaded into registers
                      once, before the first stage, so the stage loop loads
-                     weights only (k_chunk 512, K unsplit, K <= 4096,
-                     m_tiles <= 2, no token selection); 0 = the dispatcher's
+                     weights only (k_chunk 512, K unsplit, K <= 4096 and
+                     m_tiles <= 2, or K <= 9728 with m_tiles and n_tiles 1;
+                     no token selection); 0 = the dispatcher's
                      choice (the plan's when the plan uses this kernel, else
                      1).  Other kernels: ignored. */
 } krk_gemm_config;

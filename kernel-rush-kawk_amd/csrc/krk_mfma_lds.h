@@ -48,6 +48,8 @@ constexpr int kLdsNormStages = 5;
 // Most 512-k stages of x the XPRE variants hold in registers (o_proj's
 // K = 4096 with one or two x tiles); shorter K uses kLdsNormStages.
 constexpr int kLdsXpreStages = 8;
+// With one x tile and one weight tile, up to down_proj's K = 9728.
+constexpr int kLdsXpreLongStages = 19;
 
 // k per stage: 512 fits two tiles of NR + MX rows in LDS up to four 16-row
 // tiles (128 KB); 256 halves the footprint (more workgroups per CU when the
@@ -92,7 +94,8 @@ mfma_lds_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     static_assert(!(SEL && SILU), "selection reads plain logits");
     static_assert(!(NORM || XPRE) || (KC == 512 && !SEL), "x rows held in registers are whole 512-k rows");
     static_assert(!(NORM && XPRE), "the fused prologue already holds x in registers");
-    static_assert(XPRE == 0 || XPRE == kLdsNormStages || XPRE == kLdsXpreStages, "instantiated x-register depths");
+    static_assert(XPRE == 0 || XPRE == kLdsNormStages || XPRE == kLdsXpreStages || (XPRE == kLdsXpreLongStages && MT == 1 && NT == 1),
+                  "instantiated x-register depths");
     static_assert(MT >= 1 && MT <= 4, "MT covers up to 64 rows");
     static_assert(!SILU || (NT % 2 == 0), "SILU pairs gate and up tiles");
     static_assert(PF >= 2, "at least two stages in flight");

@@ -162,6 +162,11 @@ def test_x_preload_resolution(lib):
     assert resolve(24, 6144, 2560, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2
     assert resolve(20, 2560, 4096)["x_preload"] == 2  # o: 8 stages of 512 in registers
     assert resolve(40, 2560, 4096, kernel=3)["x_preload"] == 1  # three x tiles: staged with every stage
+    assert resolve(12, 2560, 9728)["x_preload"] == 2  # down: 19 stages, one x tile and one weight tile
+    for nt, ok in ((1, True), (2, False)):
+        want = GemmConfig.from_dict(dict(kernel=3, n_tiles=nt, k_chunk=512, splits=1, x_preload=2))
+        rc = lib.krk_gemm_resolve(12, 2560, 9728, NONE, ctypes.byref(want), ctypes.byref(GemmConfig()))
+        assert (rc == 0) == ok, (nt, _lib.last_error())
     for K, ok in ((4096, True), (4104, False)):  # at most 8 stages of 512
         want = GemmConfig.from_dict(dict(kernel=3, n_tiles=1, k_chunk=512, x_preload=2))
         rc = lib.krk_gemm_resolve(20, 2560, K, NONE, ctypes.byref(want), ctypes.byref(GemmConfig()))

@@ -536,12 +536,15 @@ def _lds_xpre_configs(M, silu):
                                        (24, 520, 2056, NONE), (32, 130, 512, NONE), (3, 96, 8, NONE),
                                        (13, 2 * 96, 2560, SILU), (20, 2 * 200, 1032, SILU), (32, 2 * 600, 2048, SILU),
                                        (16, 2560, 4096, NONE), (32, 2560, 4096, NONE), (9, 200, 2568, NONE),
-                                       (24, 520, 3584, NONE), (32, 2 * 300, 4096, SILU), (5, 96, 4088, NONE)])
+                                       (24, 520, 3584, NONE), (32, 2 * 300, 4096, SILU), (5, 96, 4088, NONE),
+                                       (9, 2560, 9728, NONE), (16, 200, 9000, NONE), (12, 96, 4616, NONE),
+                                       (1, 130, 9720, NONE)])
 def test_lds_x_in_registers_configs(device, M, N, K, epi):
-    """x held in registers for the whole K (one to eight 512-k stages: the
-    5-stage variant up to K = 2560, the 8-stage one above, running stages
-    past K as zeros; ragged K down to a single 8-element chunk, ragged N,
-    partial channel blocks, both epilogues) gives the oracle's results,
+    """x held in registers for the whole K (one to nineteen 512-k stages: the
+    5-stage variant up to K = 2560, the 8-stage one up to 4096 and, with one
+    x tile and one weight tile, the 19-stage one above, each running the
+    stages past K as zeros; ragged K down to a single 8-element chunk, ragged
+    N, partial channel blocks, both epilogues) gives the oracle's results,
     within the fp32 bound."""
     x = R.randn_bf16((M, K), 8780 + M)
     w = R.randn_bf16((N, K), 8781 + N, 0.02)
