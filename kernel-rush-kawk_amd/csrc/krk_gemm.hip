@@ -640,6 +640,8 @@ int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t strea
     }
     if (shm > kLdsMax || (a.splits == 1 && obcap < 1))
         return fail(KRK_ERR_UNSUPPORTED, "STREAM depth %d leaves no LDS for the output buffer", depth);
+    // The x preload stages its rows from the start of the area, before the ring.
+    if (!XF && shm < krk::stream_xstage_bytes(MT, XS)) shm = krk::stream_xstage_bytes(MT, XS);
     static std::atomic<uint64_t> done{0};
     const hipError_t attr = ensure_lds_limit(fn, (int)kLdsMax, done);
     if (attr != hipSuccess) return hip_status(attr, "stream_gemm_kernel LDS attribute");

@@ -63,6 +63,16 @@ __host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth, int nre
 // blocks, [slot][16·MT rows][CB channels].
 __host__ __device__ constexpr size_t stream_out_bytes(int MT, bool silu) { return (size_t)(silu ? 8 : 16) * 16 * MT * 2; }
 
+// x staging before the ring starts: one stage of one 16-row tile is 16 KB;
+// up to kStreamXStageMax bytes of stages go through LDS per round.
+constexpr int kStreamXStageBytes = 16 * 1024;
+constexpr size_t kStreamXStageMax = 128 * 1024;
+__host__ __device__ constexpr int stream_xgroup(int MT) { return (int)(kStreamXStageMax / ((size_t)kStreamXStageBytes * MT)); }
+// LDS the staging of XS stages needs (the launch allocates at least this).
+__host__ __device__ constexpr size_t stream_xstage_bytes(int MT, int XS) {
+    return (size_t)kStreamXStageBytes * MT * (XS < stream_xgroup(MT) ? XS : stream_xgroup(MT));
+}
+
 static_assert(kStreamKC == kFragKC, "fragment order is laid out in the stream kernel's stages");
 
 // MT: 16-row m tiles (M <= 16·MT).  XS: most K stages a workgroup owns (its
@@ -183,27 +193,36 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 XR[j][i] = (kok && m < M) ? v : u32x4{0u, 0u, 0u, 0u};
             }
         }
-        // Each stage's rows go through LDS (16·MT rows of 1 KB at the start of
-        // the area, idle until the ring starts and the first block ends;
-        // chunks XOR-swizzled by row so the fragment reads hit distinct
-        // banks) and come back as this wave's MFMA fragments X[j][kk][i].
+        // The rows go through LDS (16·MT rows of 1 KB per stage, up to XG
+        // stages at a time from the start of the area, idle until the ring
+        // starts and the first block ends; chunks XOR-swizzled by row so the
+        // fragment reads hit distinct banks) and come back as this wave's MFMA
+        // fragments X[j][kk][i]: one write, barrier, read, barrier round per
+        // group of XG stages.
+        constexpr int XG = stream_xgroup(MT);
         unsigned char* const xstage = smem;
 #pragma unroll
-        for (int j = 0; j < XS; ++j) {
+        for (int j0 = 0; j0 < XS; j0 += XG) {
 #pragma unroll
-            for (int i = 0; i < LX; ++i) {
-                const int m = wave + WV * i;
-                *reinterpret_cast<u32x4*>(xstage + m * 1024 + 16 * (lane ^ (m & 15))) = XR[j][i];
-            }
+            for (int j = j0; j < j0 + XG && j < XS; ++j)
+#pragma unroll
+                for (int i = 0; i < LX; ++i) {
+                    const int m = wave + WV * i;
+                    *reinterpret_cast<u32x4*>(xstage + (j - j0) * kStreamXStageBytes * MT + m * 1024 +
+                                              16 * (lane ^ (m & 15))) = XR[j][i];
+                }
             lds_wait();
             bare_barrier();
 #pragma unroll
-            for (int kk = 0; kk < KPW; ++kk) {
-                const int c = 4 * (wave * KPW + kk) + q;
+            for (int j = j0; j < j0 + XG && j < XS; ++j)
 #pragma unroll
-                for (int i = 0; i < MT; ++i)
-                    X[j][kk][i] = *reinterpret_cast<const u32x4*>(xstage + (16 * i + r) * 1024 + 16 * (c ^ r));
-            }
+                for (int kk = 0; kk < KPW; ++kk) {
+                    const int c = 4 * (wave * KPW + kk) + q;
+#pragma unroll
+                    for (int i = 0; i < MT; ++i)
+                        X[j][kk][i] = *reinterpret_cast<const u32x4*>(xstage + (j - j0) * kStreamXStageBytes * MT +
+                                                                      (16 * i + r) * 1024 + 16 * (c ^ r));
+                }
             lds_wait();
             bare_barrier();
         }
