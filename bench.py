@@ -10,8 +10,12 @@ a HIP graph; ``value`` is algorithmic HBM bytes per second over K steps.
 
 Also reported: the per-GEMM table of the metric (µs, GB/s, % of 8 TB/s at
 M = 1, 8, 64 for every projection, torch F.linear on the GPU timed the same
-way), the roofline of the dominant kernel, and the CPU baseline (torch bf16
-F.linear on this host's cores, the reference's own call).
+way), each projection's pure-read floor (the fastest single launch that only
+reads its weight bytes, libkrk_probe.so, swept over launch shapes), the
+roofline of the dominant kernel, and the CPU baseline (torch bf16 F.linear on
+this host's cores, the reference's own call).  The per-GEMM cells come last,
+in the log and at the end of the JSON line (``per_gemm_summary``), so a
+reader of the output's tail sees all fifteen.
 
 Algorithmic bytes per call: 2·(N_w·K + M·K + M·N_out).
 """
@@ -82,6 +86,11 @@ def main() -> int:
     ap.add_argument("--profile-shape", choices=sorted(SHAPES), default=None,
                     help="only replay one projection at --M over its distinct weights (graph of 36 launches, 8 for "
                          "lm_head, 4 replays) and a 256 MiB device copy: the counter workload of profiles/")
+    ap.add_argument("--floor", action="store_true",
+                    help="only measure the pure-read floor of every projection's weight bytes (launch-shape sweep of "
+                         "libkrk_probe.so's read kernel over the rotating weight copies) and print it as JSON")
+    ap.add_argument("--calls", type=int, default=0,
+                    help="with --profile-shape: launches per graph (default 36, 8 for lm_head)")
     ap.add_argument("--profile-dominant", action="store_true",
                     help="only replay the dominant kernel (gate_up at --M over 36 layer weights, 3 graph replays) "
                          "and a 256 MiB device copy: the workload the committed rocprofv3 --pmc summaries measure")
@@ -109,7 +118,7 @@ def main() -> int:
     if args.profile_dominant:
         return profile_dominant(torch, G, dev, args.M)
     if args.profile_shape:
-        return profile_shape(torch, G, dev, args.profile_shape, args.M)
+        return profile_shape(torch, G, dev, args.profile_shape, args.M, args.calls)
 
     # ------------------------------------------------------------ weights
     t0 = time.time()
@@ -122,6 +131,9 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"weights: {sum(t.numel() for L in layers for t in L.values()) * 2 / 1e9 + 2 * lm[0].numel() * 2 / 1e9:.2f} GB "
         f"in {time.time() - t0:.1f}s")
+    if args.floor:
+        print(json.dumps({"floor": floor_table(torch, dev, layers, lm)}), flush=True)
+        return 0
 
     # ------------------------------------------------------------ headline sweep
     M = args.M
@@ -227,8 +239,10 @@ def main() -> int:
                     tms = replay_ms(tcalls)
                     row["torch_gpu_us"] = round(tms * 1000, 2)
                 table.append(row)
-                log(f"M={Mt:3d} {name:8s} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s {row['pct_peak']:5.1f}%"
-                    + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
+        floors = floor_table(torch, dev, layers, lm)
+        for row in table:
+            row["floor_us"] = floors[row["shape"]]["us"]
+            row["x_floor"] = round(row["us"] / row["floor_us"], 3)
 
     # ------------------------------------------------------------ one GPU's 8-way tensor-parallel shard
     # The per-GPU shapes of an 8-GPU deployment (QKV, gate_up and lm_head
@@ -462,14 +476,77 @@ def main() -> int:
         "lm_head_argmax_matches_oracle": argmax_ok,
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "per_gemm": table,
         "normed": normed,
         "select": select,
         "decode_step": step_rows,
         "tp8_shard": shards,
+        "per_gemm": table,
+        # The metric's own cells, last: shape -> M -> [µs, GB/s, % of 8 TB/s,
+        # µs / pure-read floor], plus the floor µs per shape.
+        "per_gemm_summary": gemm_summary(table),
     }
+    for row in table:
+        log(f"M={row['M']:3d} {row['shape']:8s} {row['us']:8.2f} us {row['GBps']:8.1f} GB/s {row['pct_peak']:5.1f}%"
+            f"   {row['x_floor']:.2f}x the {row['floor_us']:.2f} us read floor"
+            + (f"   torch {row['torch_gpu_us']:8.2f} us" if "torch_gpu_us" in row else ""))
     print(json.dumps(result), flush=True)
     return 0
+
+
+def gemm_summary(table: list) -> dict:
+    out = {}
+    for row in table:
+        d = out.setdefault(row["shape"], {"floor_us": row["floor_us"]})
+        d[str(row["M"])] = [row["us"], row["GBps"], row["pct_peak"], row["x_floor"]]
+    return out
+
+
+PROBE_PATH = ROOT / "kernel-rush-kawk_amd" / "libkrk_probe.so"
+FLOOR_BLOCKS = (256, 512, 1024, 2048)
+FLOOR_UNROLL = (4, 8, 16)
+
+
+def floor_table(torch, dev, layers, lm) -> dict:
+    """Pure-read floor of each projection's weight bytes: libkrk_probe.so's
+    read kernel (krk_probe_read: workgroups of 512 threads each streaming a
+    contiguous chunk with 16-byte nontemporal loads, `unroll` loads in flight
+    per thread, nothing else) swept over FLOOR_BLOCKS x FLOOR_UNROLL, each
+    launch shape timed like the GEMMs (graph replay over the same rotating
+    weight copies); the fastest launch per shape."""
+    import ctypes
+
+    from kernels.timing import replay_ms
+
+    if not PROBE_PATH.exists():
+        raise RuntimeError(f"{PROBE_PATH} is missing: build it with __graft_entry__.build()")
+    probe = ctypes.CDLL(str(PROBE_PATH))
+    probe.krk_probe_read.restype = ctypes.c_int
+    probe.krk_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_void_p]
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    out = {}
+    for name in SHAPES:
+        ws = lm if name == "lm_head" else [L[name] for L in layers]
+        nbytes = ws[0].numel() * ws[0].element_size()
+        n = max(MIN_CALLS, len(ws))
+        best = None
+        for blocks in FLOOR_BLOCKS:
+            for unroll in FLOOR_UNROLL:
+                def read(w, blocks=blocks, unroll=unroll):
+                    rc = probe.krk_probe_read(w.data_ptr(), nbytes, sink.data_ptr(), blocks, unroll,
+                                              torch.cuda.current_stream().cuda_stream)
+                    if rc:
+                        raise RuntimeError(f"krk_probe_read failed ({rc})")
+                ms = replay_ms([(lambda w=ws[i % len(ws)]: read(w)) for i in range(n)])
+                if best is None or ms < best[0]:
+                    best = (ms, blocks, unroll)
+        ms, blocks, unroll = best
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"bytes": nbytes, "us": round(ms * 1000, 2), "GBps": round(gbps, 1),
+                     "pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "blocks": blocks, "unroll": unroll}
+        log(f"read floor {name:8s} {nbytes / 1e6:7.2f} MB  {ms * 1000:8.2f} us  {gbps:7.1f} GB/s "
+            f"({blocks} workgroups, {unroll} loads in flight per thread)")
+    return out
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "stream_gemm_gate_up_M32_traffic.json"
@@ -489,18 +566,22 @@ def measured_traffic(name: str, M: int, config: dict):
     return rec.get("traffic_bytes_per_launch")
 
 
-def profile_shape(torch, G, dev, name: str, M: int) -> int:
+def profile_shape(torch, G, dev, name: str, M: int, calls: int = 0) -> int:
     """Workload for the counter runs: replays of a graph of launches of one
     projection over distinct weights (the 36 layer weights of the sweep; for
-    lm_head 2 copies, 8 launches), then 4 copies of a 256 MiB buffer for the
-    counters' byte calibration.  Prints the configuration and the event-timed
-    µs per launch of the graph (median of 3 replays, after the timer's ~10 ms
-    of untimed ones)."""
+    lm_head 2 copies, 8 launches; ``calls`` launches when given, cycling the
+    copies), then 4 copies of a 256 MiB buffer for the counters' byte
+    calibration.  Prints the configuration and the event-timed µs per launch
+    of the graph (median of 3 replays, after the timer's ~10 ms of untimed
+    ones)."""
     K, Nw, silu = SHAPES[name]
     if name == "lm_head":
-        ws = [randn_bf16(torch, (Nw, K), seed_for(4, 99, "lm_head") + i, 0.02, dev) for i in range(2)] * 4
+        ws = [randn_bf16(torch, (Nw, K), seed_for(4, 99, "lm_head") + i, 0.02, dev) for i in range(2)]
+        ws = ws * 4
     else:
         ws = [randn_bf16(torch, (Nw, K), seed_for(4, l, name), 0.02, dev) for l in range(LAYERS)]
+    if calls > 0:
+        ws = [ws[i % len(ws)] for i in range(calls)]
     x = randn_bf16(torch, (M, K), seed_for(4, 0, "x") + K, 1.0, dev)
     op = G.SkinnyGateUp(M, Nw // 2, K, dev) if silu else G.SkinnyMatmul(M, Nw, K, dev)
     out = torch.empty((M, Nw // 2 if silu else Nw), dtype=torch.bfloat16, device=dev)

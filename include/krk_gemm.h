@@ -334,8 +334,8 @@ int krk_gemm_select_fused(int M, int N, int K, int k, const krk_gemm_config* cfg
  * krk_gemm_bf16_noalloc — krk_gemm_bf16 without a workspace argument, for
  * callers that cannot allocate device memory (code under HIP graph capture
  * that may not call hipMalloc, tight serving loops, harnesses that forbid
- * allocation).  No counterpart in the reference: its kernels allocate their
- * split-K partials per object (engine/kernels/gemm.py:341).
+ * allocation).  This entry point has no counterpart in the reference; it
+ * exists for those callers, which cannot allocate.
  *
  * The split-K counters and partials live in a static device array of
  * KRK_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
@@ -354,6 +354,23 @@ int krk_gemm_bf16_noalloc(const void* x, int64_t ldx,
                           void* y, int64_t ldy,
                           int M, int N, int K, int epilogue,
                           void* stream);
+
+/*
+ * ABI identification, for bindings that lay out krk_gemm_config themselves
+ * (a ctypes / cgo / JNI stub).  No counterpart in the reference: its kernels
+ * are Python objects with no binary interface.
+ *
+ * krk_abi_version — KRK_ABI_VERSION of the built library.  The version moves
+ *   whenever a declaration or the krk_gemm_config layout changes (version 3:
+ *   the ten-int krk_gemm_config above, prologue/channels/x_preload added to
+ *   version 1's seven ints).
+ * krk_gemm_config_size — sizeof(krk_gemm_config) in the built library.  A
+ *   binding must check both at load time and refuse a mismatch: a config
+ *   array of another layout would be over- or under-read.
+ */
+#define KRK_ABI_VERSION 3
+int krk_abi_version(void);
+size_t krk_gemm_config_size(void);
 
 /*
  * krk_last_error — text of the last error raised on the calling thread by

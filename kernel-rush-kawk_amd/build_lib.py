@@ -1,8 +1,10 @@
-"""Build libkrk_gemm.so (the C-ABI GEMM library) for gfx950 with hipcc.
+"""Build libkrk_gemm.so (the C-ABI GEMM library) and libkrk_probe.so (the
+pure-read floor probe bench.py measures against) for gfx950 with hipcc.
 
-Usage: ``python kernel-rush-kawk_amd/build_lib.py`` (or ``build()`` from
-Python).  The library is written next to this file so it ships with the tree.
-hipcc cross-compiles for gfx950 without a GPU present.
+Usage: ``python kernel-rush-kawk_amd/build_lib.py`` (or ``build()`` /
+``build_probe()`` from Python).  The libraries are written next to this file
+so they ship with the tree.  hipcc cross-compiles for gfx950 without a GPU
+present.
 """
 
 from __future__ import annotations
@@ -17,6 +19,8 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libkrk_gemm.so"
 SOURCES = [CSRC / "krk_gemm.hip"]
+PROBE_LIB = HERE / "libkrk_probe.so"
+PROBE_SOURCES = [CSRC / "krk_probe.hip"]
 HEADERS = sorted(CSRC.glob("*.h")) + [ROOT / "include" / "krk_gemm.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -36,11 +40,13 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None) -> Path:
-    """Compile the library; always recompiles.  Returns the library path."""
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None,
+          sources: list[Path] | None = None) -> Path:
+    """Compile the GEMM library (or ``sources`` into ``out``); always
+    recompiles.  Returns the library path."""
     out = Path(out) if out else LIB
     tmp = out.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, *(extra_flags or []), *map(str, SOURCES), "-o", str(tmp)]
+    cmd = [HIPCC, *FLAGS, *(extra_flags or []), *map(str, sources or SOURCES), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -56,7 +62,13 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path
     return out
 
 
+def build_probe(verbose: bool = False) -> Path:
+    """Compile libkrk_probe.so (bench.py's pure-read floor); always recompiles."""
+    return build(verbose, out=PROBE_LIB, sources=PROBE_SOURCES)
+
+
 if __name__ == "__main__":
     path = build(verbose=True)
     print(f"built {path}")
+    print(f"built {build_probe(verbose=True)}")
     sys.exit(0)

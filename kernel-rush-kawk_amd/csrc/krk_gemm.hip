@@ -1598,4 +1598,8 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
 
 const char* krk_last_error(void) { return g_err; }
 
+int krk_abi_version(void) { return KRK_ABI_VERSION; }
+
+size_t krk_gemm_config_size(void) { return sizeof(krk_gemm_config); }
+
 }  // extern "C"

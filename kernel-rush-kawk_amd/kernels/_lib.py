@@ -103,7 +103,12 @@ SIGNATURES = {
                                       _int, _int, _int, _int, _c_void_p]),
     "krk_gemm_candidates": (_int, [_int, _int, _int, _int, ctypes.POINTER(GemmConfig), _int]),
     "krk_last_error": (ctypes.c_char_p, []),
+    "krk_abi_version": (_int, []),
+    "krk_gemm_config_size": (_size, []),
 }
+
+#: The ABI this binding was written against (KRK_ABI_VERSION in include/krk_gemm.h).
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()
@@ -123,6 +128,11 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            abi, size = lib.krk_abi_version(), lib.krk_gemm_config_size()
+            if abi != ABI_VERSION or size != ctypes.sizeof(GemmConfig):
+                raise ImportError(f"{LIB_PATH}: ABI version {abi} with a {size}-byte krk_gemm_config; this binding "
+                                  f"expects version {ABI_VERSION} and {ctypes.sizeof(GemmConfig)} bytes (rebuild the "
+                                  "library or update the binding)")
             _lib = lib
     return _lib
 

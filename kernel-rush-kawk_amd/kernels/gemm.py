@@ -463,13 +463,43 @@ def _validation_plan(M: int, epilogue: int, w, rot: list):
     return checks, strict
 
 
+def _down_for(checks: list, w, rot: list, down) -> list:
+    """The down-projection weight that consumes each checked gate/up weight's
+    output: ``down`` is one ``[K_out, I]`` weight, or a list aligned with the
+    rotation (layer i's down weight for layer i's gate/up weight; ``w``
+    itself pairs with ``down[0]`` when it is not in the rotation)."""
+    if down is None:
+        return []
+    if isinstance(down, torch.Tensor):
+        return [down] * len(checks)
+    if len(down) != len(rot):
+        raise ValueError(f"down: {len(down)} weights for a rotation of {len(rot)}")
+    pair = {id(v): d for v, d in zip(rot, down)}
+    return [pair.get(id(v), down[0]) for v in checks]
+
+
+def downstream_ok(out: torch.Tensor, ref: torch.Tensor, wd: torch.Tensor) -> tuple[bool, str]:
+    """The consumer check of the reference's N32 gate/up selector
+    (engine/kernels/m64_gateup_n32_selection.py:73-105): the candidate's
+    gate/up output and the reference's, each run through the same down
+    projection (fp32-accumulated torch), must agree under the pointwise
+    M = 64 rule."""
+    from . import tune
+
+    ok, why = tune.pointwise_ok(_linear_fp32acc(out, wd), _linear_fp32acc(ref, wd))
+    return ok, ("down projection: " + why)
+
+
 def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_NONE, ws: list | None = None,
-                    log=None, cache=None, norm=None, limit: int | None = None):
+                    log=None, cache=None, norm=None, limit: int | None = None, down=None):
     """Tune the projection ``a @ w.T`` (with ``epilogue``, and with the
     residual-add + RMSNorm prologue when ``norm=(y, w_norm, eps)``) over the
     library's candidate configurations on this GPU, timing each as a graph
     replay over ``ws``.  Returns a :class:`kernels.tune.Result`; the chosen
-    configuration is cached (``cache``, default :func:`kernels.tune.default_cache`)."""
+    configuration is cached (``cache``, default :func:`kernels.tune.default_cache`).
+    ``down``: for a gate/up projection, the down weight(s) that consume its
+    output (one tensor, or a list aligned with ``ws``); at 64 rows or more
+    each candidate's output must also pass :func:`downstream_ok`."""
     from . import tune
 
     M, K = a.shape
@@ -480,11 +510,14 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
     # Candidates are validated against each weight's own fp32-accumulated
     # torch result (which weights, and which rules: _validation_plan).
     checks, strict = _validation_plan(M, epilogue, w, rot)
+    downs = _down_for(checks, w, rot, down) if strict else []
 
-    def judge(out, ref):
+    def judge(out, ref, i=0):
         ok, why = tune.close_ok(out, ref)
         if ok and strict:
             ok, why = tune.pointwise_ok(out, ref)
+        if ok and downs:
+            ok, why = downstream_ok(out, ref, downs[i])
         return ok, why
 
     def project(inp, weight):
@@ -499,8 +532,8 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
             return lambda w_: mm(a, w_)
 
         def accept(fn):
-            for v, ref in zip(checks, refs):
-                ok, why = judge(fn(v), ref)
+            for i, (v, ref) in enumerate(zip(checks, refs)):
+                ok, why = judge(fn(v), ref, i)
                 if not ok:
                     return ok, why
             return ok, why
@@ -516,12 +549,12 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
             return lambda w_: mm(a, w_, norm=(y, w_norm, xout, eps))
 
         def accept(fn):
-            for v, ref in zip(checks, refs):
+            for i, (v, ref) in enumerate(zip(checks, refs)):
                 xout.fill_(0)
                 out = fn(v)
                 if not torch.equal(xout, ref_xout):
                     return False, "xout differs from x + y"
-                ok, why = judge(out, ref)
+                ok, why = judge(out, ref, i)
                 if not ok:
                     return ok, why
             return ok, why
@@ -557,13 +590,15 @@ def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = No
     return mm
 
 
-def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = None, tune: bool = True, cache=None):
+def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = None, tune: bool = True, cache=None,
+                down=None):
     """Return ``f(a, wgu) -> silu(a @ Wg.T) * (a @ Wu.T)`` (reference
     engine/kernels/gemm.py:461-498), tuned like :func:`pick_matmul` and
-    validated against ``swiglu(F.linear)``."""
+    validated against ``swiglu(F.linear)``.  ``down``: the down weight(s)
+    consuming the output (see :func:`tune_projection`)."""
     M, K = a.shape
     I = wgu.shape[0] // 2
-    cfg = tune_projection(a, wgu, EPILOGUE_SILU_MUL, ws, log, cache).config if tune else None
+    cfg = tune_projection(a, wgu, EPILOGUE_SILU_MUL, ws, log, cache, down=down).config if tune else None
     mm = SkinnyGateUp(M, I, K, a.device, config=cfg)
     _validate(mm(a, wgu), _silu_mul(_linear_fp32acc(a, wgu)), f"gateup M={M} I={I} K={K}", log)
     if log:
@@ -583,7 +618,7 @@ def _add_rms_norm_ref(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, ep
 
 
 def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, w: torch.Tensor, eps: float,
-                log=None, ws: list | None = None, tune: bool = True, cache=None):
+                log=None, ws: list | None = None, tune: bool = True, cache=None, down=None):
     """Return ``f(x, y, w_norm, xout, w) -> proj(rms_norm(x + y))`` that also
     writes ``xout = x + y`` (reference engine/kernels/gemm.py:501-560).
     ``kind`` is "matmul" or "gateup".  Tuned like :func:`pick_matmul` over
@@ -591,13 +626,15 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
     configuration runs it), then validated once against the torch
     composition (xout bit-exact, projection under :func:`_validate`'s rule);
     with ``log`` the graph-replay time is logged.  Without tuning the
-    library's normed plan runs."""
+    library's normed plan runs.  ``down`` (gate/up only): the down weight(s)
+    consuming the output, checked at 64 rows or more (:func:`tune_projection`)."""
     if kind not in ("matmul", "gateup"):
         raise ValueError(f"kind must be 'matmul' or 'gateup', got {kind!r}")
     M, K = x.shape
     N = w.shape[0]
     epi = EPILOGUE_SILU_MUL if kind == "gateup" else EPILOGUE_NONE
-    cfg = tune_projection(x, w, epi, ws, log, cache, norm=(y, w_norm, eps)).config if tune else None
+    cfg = tune_projection(x, w, epi, ws, log, cache, norm=(y, w_norm, eps),
+                          down=down if kind == "gateup" else None).config if tune else None
     mm = _projection(M, N, K, epi, x.device, cfg)
     fn = lambda x_, y_, wn_, xout_, w_: mm(x_, w_, norm=(y_, wn_, xout_, eps))
     xout = torch.empty_like(x)

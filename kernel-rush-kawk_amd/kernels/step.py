@@ -42,7 +42,10 @@ from . import gemm as G
 
 def decode_matmuls(m, M: int, log=None, tune: bool = True, select_k: int | None = None) -> dict:
     """Per-shape projection callables for M-row decode steps (reference
-    engine/model.py:137-178)."""
+    engine/model.py:137-178).  The gate/up pickers get each layer's down
+    weight, so at 64 rows a tuned gate/up configuration is also checked
+    through the down projection that consumes it (the reference's N32
+    selector, engine/kernels/m64_gateup_n32_selection.py:73-105)."""
     cfg = m.cfg
     layer = m.layers[0]
     L = m.layers
@@ -55,7 +58,7 @@ def decode_matmuls(m, M: int, log=None, tune: bool = True, select_k: int | None 
     eps = cfg.eps
     if os.environ.get("ENGINE_NORM_FUSED", "1") != "1":
         qkv = G.pick_matmul(x, layer.wqkv, log, ws=[l.wqkv for l in L], tune=tune)
-        gu = G.pick_gateup(x, layer.wgu, log, ws=[l.wgu for l in L], tune=tune)
+        gu = G.pick_gateup(x, layer.wgu, log, ws=[l.wgu for l in L], tune=tune, down=[l.wd for l in L])
         lm = G.pick_matmul(x, m.lm_head, log, tune=tune)
         mm = {
             "qkv": lambda x, y, wn, xout, w: qkv(G.add_rms_norm(x, y, wn, eps, xout), w),
@@ -68,7 +71,8 @@ def decode_matmuls(m, M: int, log=None, tune: bool = True, select_k: int | None 
         mm = {
             "qkv": G.pick_normed("matmul", x, y, layer.in_norm, layer.wqkv, eps, log, ws=[l.wqkv for l in L], tune=tune),
             "o": G.pick_matmul(a, layer.wo, log, ws=[l.wo for l in L], tune=tune),
-            "gu": G.pick_normed("gateup", x, y, layer.post_norm, layer.wgu, eps, log, ws=[l.wgu for l in L], tune=tune),
+            "gu": G.pick_normed("gateup", x, y, layer.post_norm, layer.wgu, eps, log, ws=[l.wgu for l in L], tune=tune,
+                                down=[l.wd for l in L]),
             "d": G.pick_matmul(act, layer.wd, log, ws=[l.wd for l in L], tune=tune),
             "lm": G.pick_normed("matmul", x, y, m.final_norm, m.lm_head, eps, log, tune=tune),
         }

@@ -19,13 +19,22 @@ as a graph replay over every layer's copy of the weight
   configuration computes the same function);
 * timing is :func:`kernels.timing.replay_ms` (graph replay, median of 5,
   rotating weights);
+* the plan stays unless a challenger beats it by the reference's M = 64
+  margin: the fastest few candidates of the sweep are timed again against
+  the plan in both orders (plan first, then challenger first), and one
+  replaces the plan only if both ratios are below ``MARGIN`` = 0.97
+  (engine/kernels/m64_gateup_selection.py:100-128); the challenger with the
+  lowest worst ratio wins;
 * results go to a ``TuneCache`` keyed by GPU architecture, library build,
   kind and shape, optionally persisted as JSON (``KRK_TUNE_CACHE``), so a
   serving process tunes once per shape and later processes with the same
   library start from the file.
 
 The winner is always a HIP configuration: torch is not a candidate, so a
-tuned call never leaves the native path.
+tuned call never leaves the native path.  Where the reference keeps cuBLAS
+when no candidate validates (engine/kernels/gemm.py:449-452), a search here
+whose plan fails validation raises: every configuration computes the same
+function, so a failing plan is a library fault, not a slower candidate.
 
 Command line (from the package directory, GPU required)::
 
@@ -122,6 +131,39 @@ class Result:
     plan_us: float | None     # the dispatch table's configuration, when measured
     cached: bool = False
     trials: list = field(default_factory=list)
+    # (challenger config, ratio with the plan timed first, ratio with the
+    # challenger timed first) for every challenger confirmed against the plan
+    confirmations: list = field(default_factory=list)
+
+
+# A challenger replaces the plan only when it takes less than this fraction
+# of the plan's time in each of two opposite-order timings
+# (engine/kernels/m64_gateup_selection.py:124-128).
+MARGIN = 0.97
+# Fastest challengers of the sweep that are confirmed against the plan.
+CONFIRM = 3
+
+
+def confirm_ratios(plan_fn, cand_fn, timer, rot) -> tuple[float, float] | None:
+    """Challenger / plan time ratios from two opposite-order timings: plan
+    then challenger, then challenger then plan (the reference's
+    ``candidate_first in (False, True)`` loop, m64_gateup_selection.py:100-120).
+    None when a timing is not a positive finite number or the budget ran out
+    (the plan is kept)."""
+    import math
+
+    ratios = []
+    for cand_first in (False, True):
+        times = {}
+        for which in (("cand", "plan") if cand_first else ("plan", "cand")):
+            if budget.expired():
+                return None
+            ms = timer(cand_fn if which == "cand" else plan_fn, rot)
+            if not (isinstance(ms, (int, float)) and math.isfinite(ms) and ms > 0):
+                return None
+            times[which] = ms
+        ratios.append(times["cand"] / times["plan"])
+    return ratios[0], ratios[1]
 
 
 def close_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
@@ -186,7 +228,11 @@ def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, acce
     followed by ``extra``; ``plan`` replaces the library's plan at the head
     (the normed calls' own plan).  The plan (first candidate) is always
     measured; the rest while the budget lasts (at most ``limit`` candidates
-    in all when given)."""
+    in all when given).  The ``CONFIRM`` fastest candidates that beat the
+    plan's sweep time are then timed against it in both orders
+    (:func:`confirm_ratios`); the plan is kept unless one of them clears
+    ``MARGIN`` in both.  If the plan itself is rejected or cannot be timed,
+    the fastest validated candidate is taken as it stands."""
     key = TuneCache.key(device, kind, M, N, K) if cache is not None else None
     if cache is not None:
         hit = cache.get(key)
@@ -200,8 +246,9 @@ def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, acce
     if limit is not None:
         cands = cands[:max(1, limit)]
     trials: list[Trial] = []
-    best: tuple[float, dict] | None = None
+    timed: list[tuple[float, int, dict, object]] = []  # (us, sweep index, config, fn)
     plan_us = None
+    plan_fn = None
     for i, cfg in enumerate(cands):
         if i > 0 and budget.expired():
             break
@@ -219,12 +266,28 @@ def search(kind: str, M: int, N: int, K: int, epilogue: int, device, build, acce
             continue
         trials.append(Trial(cfg, us))
         if i == 0:
-            plan_us = us
-        if best is None or us < best[0]:
-            best = (us, cfg)
-    if best is None:
+            plan_us, plan_fn = us, fn
+        timed.append((us, i, cfg, fn))
+    if not timed:
         raise RuntimeError(f"tune {kind} M={M} N={N} K={K}: no candidate passed validation")
-    res = Result(best[1], best[0], plan_us, trials=trials)
+    timed.sort(key=lambda t: (t[0], t[1]))
+    confirmations = []
+    if plan_fn is None:
+        # No incumbent to beat: the fastest validated candidate as timed.
+        best_us, _, best_cfg, _ = timed[0]
+    else:
+        best_us, best_cfg, best_ratio = plan_us, cands[0], 1.0
+        for us, _, cfg, fn in [t for t in timed if t[1] != 0 and t[0] < plan_us][:CONFIRM]:
+            r = confirm_ratios(plan_fn, fn, timer, rot)
+            if r is None:
+                break
+            confirmations.append((cfg, r[0], r[1]))
+            worst = max(r)
+            if log:
+                log(f"tune {kind} M={M} N={N} K={K}: krk{cfg} against the plan {r[0]:.4f} / {r[1]:.4f}")
+            if worst < MARGIN and worst < best_ratio:
+                best_us, best_cfg, best_ratio = us, cfg, worst
+    res = Result(best_cfg, best_us, plan_us, trials=trials, confirmations=confirmations)
     if cache is not None:
         cache.put(key, res.config, res.us)
     if log:

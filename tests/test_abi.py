@@ -41,6 +41,27 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name), f"{name} is declared in krk_gemm.h but not exported"
 
 
+def test_abi_version_and_config_layout(lib):
+    """The library reports the header's KRK_ABI_VERSION and its
+    krk_gemm_config size, and the binding checks both when it loads: a
+    binding of another layout would read past, or short of, a config array."""
+    version = int(re.search(r"#define KRK_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.krk_abi_version() == version == _lib.ABI_VERSION
+    fields = re.search(r"typedef struct krk_gemm_config \{(.*?)\} krk_gemm_config;", HEADER.read_text(), re.S).group(1)
+    ints = re.findall(r"^\s*int\s+(\w+);", fields, re.M)
+    assert ints == [name for name, _ in GemmConfig._fields_]
+    assert lib.krk_gemm_config_size() == ctypes.sizeof(GemmConfig) == 4 * len(ints)
+
+
+def test_binding_refuses_another_abi(monkeypatch):
+    """_lib.load() raises ImportError when the library's ABI version differs
+    from the binding's (here: the binding pretends to expect version 2)."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", 2)
+    with pytest.raises(ImportError, match="ABI version 3"):
+        _lib.load()
+
+
 def call(lib, x=X, ldx=2560, w=W, ldw=2560, y=Y, ldy=None, M=1, N=6144, K=2560, epi=NONE, ws=0, wsb=0):
     if ldy is None:
         ldy = N // 2 if epi == SILU else N

@@ -255,3 +255,98 @@ def test_validation_plan_of_the_tuner():
     assert checks == [w] + rot and strict
     checks, strict = _validation_plan(64, EPILOGUE_SILU_MUL, w, [w])
     assert checks == [w] and strict
+
+
+def _margin_search(times_of, order_bias=None):
+    """tune.search over the real candidate list of qkv at M = 8 with stub
+    build / acceptance and a timer that returns ``times_of(index)`` for the
+    candidate at that index of the list (the plan is index 0); with
+    ``order_bias(index, call)`` the timer also sees how many timings came
+    before, so a test can make a result depend on the order."""
+    from kernels import budget, tune
+
+    budget.use(None)
+    budget.clear()
+    cands = tune.candidates(8, 6144, 2560, 0)
+    index = {id(c): i for i, c in enumerate(cands)}
+    calls = []
+
+    def build(cfg):
+        i = next(j for j, c in enumerate(cands) if c == cfg)
+        return lambda w: i
+
+    def timer(fn, rot):
+        i = fn(None)
+        calls.append(i)
+        t = times_of(i)
+        return t * (order_bias(i, len(calls)) if order_bias else 1.0)
+
+    res = tune.search("matmul", 8, 6144, 2560, 0, "cpu", build, lambda fn: (True, ""), timer, [None], cache=None)
+    return res, cands, calls
+
+
+def test_challenger_two_percent_faster_keeps_the_plan():
+    """A candidate 2% faster than the plan in both orders does not clear the
+    reference's 3% margin (m64_gateup_selection.py:124-128)."""
+    res, cands, _ = _margin_search(lambda i: 1.0 if i == 0 else (0.98 if i == 3 else 1.2))
+    assert res.config == cands[0] and res.us == res.plan_us == 1000.0
+    assert [c[0] for c in res.confirmations] == [cands[3]]
+    assert all(abs(r - 0.98) < 1e-9 for r in res.confirmations[0][1:])
+
+
+def test_challenger_five_percent_faster_replaces_the_plan():
+    res, cands, calls = _margin_search(lambda i: 1.0 if i == 0 else (0.95 if i == 5 else 1.2))
+    assert res.config == cands[5] and abs(res.us - 950.0) < 1e-6 and res.plan_us == 1000.0
+    # the sweep, then plan/challenger and challenger/plan
+    assert calls[-4:] == [0, 5, 5, 0]
+
+
+def test_challenger_must_clear_the_margin_in_both_orders():
+    """5% faster when timed after the plan, 1.2% when timed first: kept out."""
+
+    def times(i):
+        return 1.0 if i == 0 else (0.95 if i == 4 else 1.2)
+
+    res, cands, calls = _margin_search(times, order_bias=lambda i, n: 1.0)
+    assert res.config == cands[4]
+    # the sweep takes one timing per candidate; the challenger-first timing
+    # of candidate 4 is then call len(cands) + 3
+    n_sweep = len(calls)
+    res, cands, calls = _margin_search(times, order_bias=lambda i, n: 1.04 if (i == 4 and n == n_sweep - 1) else 1.0)
+    r1, r2 = res.confirmations[0][1:]
+    assert r1 < 0.97 <= r2 and res.config == cands[0]
+
+
+def test_best_of_several_challengers_by_worst_ratio():
+    res, cands, _ = _margin_search(lambda i: {0: 1.0, 2: 0.96, 6: 0.90, 7: 0.93}.get(i, 1.3))
+    assert res.config == cands[6]
+    assert [c[0] for c in res.confirmations] == [cands[6], cands[7], cands[2]]
+
+
+def test_downstream_check_of_gateup_candidates():
+    """At 64 rows a gate/up candidate is also judged through the down
+    projection that consumes it (m64_gateup_n32_selection.py:73-105): the
+    down weights pair with the rotation's gate/up weights by position."""
+    import torch
+
+    from kernels.gemm import _down_for, downstream_ok
+
+    g = torch.Generator().manual_seed(5)
+    ref = torch.randn((64, 96), generator=g).to(torch.bfloat16)
+    wd = (torch.randn((40, 96), generator=g) * 0.05).to(torch.bfloat16)
+    assert downstream_ok(ref.clone(), ref, wd)[0]
+    bad = ref.clone()
+    bad[7] = bad[7] * 1.3                      # one whole row 30% off: the down rows move with it
+    ok, why = downstream_ok(bad, ref, wd)
+    assert not ok and why.startswith("down projection")
+    w, rot = object(), [object() for _ in range(3)]
+    downs = ["d0", "d1", "d2"]
+    assert _down_for([rot[1], rot[2]], rot[1], rot, downs) == ["d1", "d2"]
+    assert _down_for([w, rot[0]], w, rot, downs) == ["d0", "d0"]
+    assert _down_for([w], w, rot, None) == []
+    t = torch.zeros(1)
+    assert _down_for([w, rot[0]], w, rot, t) == [t, t]
+    import pytest
+
+    with pytest.raises(ValueError):
+        _down_for([w], w, rot, ["d0"])
