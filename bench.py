@@ -502,17 +502,19 @@ def gemm_summary(table: list) -> dict:
 
 
 PROBE_PATH = ROOT / "kernel-rush-kawk_amd" / "libkrk_probe.so"
-FLOOR_BLOCKS = (256, 512, 1024, 2048)
-FLOOR_UNROLL = (4, 8, 16)
+FLOOR_BLOCKS = (256, 512, 1024, 2048, 4096)
+FLOOR_UNROLL = (2, 4, 8, 16)
+FLOOR_ORDER = ("chunked", "interleaved")
 
 
 def floor_table(torch, dev, layers, lm) -> dict:
     """Pure-read floor of each projection's weight bytes: libkrk_probe.so's
-    read kernel (krk_probe_read: workgroups of 512 threads each streaming a
-    contiguous chunk with 16-byte nontemporal loads, `unroll` loads in flight
-    per thread, nothing else) swept over FLOOR_BLOCKS x FLOOR_UNROLL, each
-    launch shape timed like the GEMMs (graph replay over the same rotating
-    weight copies); the fastest launch per shape."""
+    read kernel (krk_probe_read: workgroups of 512 threads streaming 16-byte
+    nontemporal loads, each workgroup one contiguous chunk or groups taken in
+    turn, `unroll` loads in flight per thread, nothing else) swept over
+    FLOOR_ORDER x FLOOR_BLOCKS x FLOOR_UNROLL, each launch shape timed like
+    the GEMMs (graph replay over the same rotating weight copies); the
+    fastest launch per shape."""
     import ctypes
 
     from kernels.timing import replay_ms
@@ -522,7 +524,7 @@ def floor_table(torch, dev, layers, lm) -> dict:
     probe = ctypes.CDLL(str(PROBE_PATH))
     probe.krk_probe_read.restype = ctypes.c_int
     probe.krk_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
-                                     ctypes.c_void_p]
+                                     ctypes.c_int, ctypes.c_void_p]
     sink = torch.zeros(256, dtype=torch.int32, device=dev)
     out = {}
     for name in SHAPES:
@@ -530,22 +532,24 @@ def floor_table(torch, dev, layers, lm) -> dict:
         nbytes = ws[0].numel() * ws[0].element_size()
         n = max(MIN_CALLS, len(ws))
         best = None
-        for blocks in FLOOR_BLOCKS:
-            for unroll in FLOOR_UNROLL:
-                def read(w, blocks=blocks, unroll=unroll):
-                    rc = probe.krk_probe_read(w.data_ptr(), nbytes, sink.data_ptr(), blocks, unroll,
-                                              torch.cuda.current_stream().cuda_stream)
-                    if rc:
-                        raise RuntimeError(f"krk_probe_read failed ({rc})")
-                ms = replay_ms([(lambda w=ws[i % len(ws)]: read(w)) for i in range(n)])
-                if best is None or ms < best[0]:
-                    best = (ms, blocks, unroll)
-        ms, blocks, unroll = best
+        for order in FLOOR_ORDER:
+            for blocks in FLOOR_BLOCKS:
+                for unroll in FLOOR_UNROLL:
+                    def read(w, blocks=blocks, unroll=unroll, inter=int(order == "interleaved")):
+                        rc = probe.krk_probe_read(w.data_ptr(), nbytes, sink.data_ptr(), blocks, unroll, inter,
+                                                  torch.cuda.current_stream().cuda_stream)
+                        if rc:
+                            raise RuntimeError(f"krk_probe_read failed ({rc})")
+                    ms = replay_ms([(lambda w=ws[i % len(ws)]: read(w)) for i in range(n)])
+                    if best is None or ms < best[0]:
+                        best = (ms, order, blocks, unroll)
+        ms, order, blocks, unroll = best
         gbps = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"bytes": nbytes, "us": round(ms * 1000, 2), "GBps": round(gbps, 1),
-                     "pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "blocks": blocks, "unroll": unroll}
+                     "pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 1), "order": order, "blocks": blocks,
+                     "unroll": unroll}
         log(f"read floor {name:8s} {nbytes / 1e6:7.2f} MB  {ms * 1000:8.2f} us  {gbps:7.1f} GB/s "
-            f"({blocks} workgroups, {unroll} loads in flight per thread)")
+            f"({order}, {blocks} workgroups, {unroll} loads in flight per thread)")
     return out
 
 
