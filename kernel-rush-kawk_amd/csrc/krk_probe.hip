@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "krk_probe.h"
+
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;

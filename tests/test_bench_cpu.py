@@ -46,3 +46,26 @@ def test_traffic_record_matches_the_dominant_plan():
     assert rec["config"] == cfg
     assert bench.measured_traffic("gate_up", 32, cfg) == rec["traffic_bytes_per_launch"]
     assert 1.0 <= rec["traffic_bytes_per_launch"] / rec["algorithmic_bytes_per_launch"] < 1.1
+
+
+def test_probe_library_exports_and_checks_arguments():
+    """libkrk_probe.so (bench.py's pure-read floor) exports the function
+    include/krk_probe.h declares and rejects bad arguments before any
+    launch (no GPU is touched here)."""
+    import ctypes
+    import re
+
+    lib_path = ROOT / "kernel-rush-kawk_amd" / "libkrk_probe.so"
+    header = (ROOT / "include" / "krk_probe.h").read_text()
+    declared = set(re.findall(r"\b(krk_\w+)\s*\(", re.sub(r"/\*.*?\*/", "", header, flags=re.S)))
+    assert declared == {"krk_probe_read"}
+    lib = ctypes.CDLL(str(lib_path))
+    f = lib.krk_probe_read
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_void_p]
+    P, S = 0x10000000, 0x20000000  # never dereferenced: every case fails its checks first
+    for args in [(0, 1024, S, 256, 8, 0), (P, 1000, S, 256, 8, 0), (P + 8, 1024, S, 256, 8, 0),
+                 (P, 1024, 0, 256, 8, 0), (P, 1024, S, 0, 8, 0), (P, 1024, S, 70000, 8, 0),
+                 (P, 1024, S, 256, 3, 1), (P, 0, S, 256, 8, 1)]:
+        assert f(*args, None) == -1, args
