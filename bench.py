@@ -49,7 +49,8 @@ SHAPES = {
 }
 TENSOR_ID = {"x": 0, "qkv": 1, "o": 2, "gate_up": 3, "down": 4, "lm_head": 5}
 # krk_gemm_config.kernel -> device function name (as rocprofv3 reports it)
-KERNEL_NAMES = {1: "mfma_gemm_kernel", 2: "valu_gemm_kernel", 3: "mfma_lds_kernel", 5: "stream_gemm_kernel"}
+KERNEL_NAMES = {1: "mfma_gemm_kernel", 2: "valu_gemm_kernel", 3: "mfma_lds_kernel", 5: "stream_gemm_kernel",
+                6: "slice_gemm_kernel"}
 
 
 def log(*a):

@@ -100,7 +100,9 @@ enum {
     KRK_KERNEL_VALU = 2,   /* dot2 row streaming in 512-k blocks (M <= 8); x in registers
                               (M <= 2) or staged once in LDS (M > 2) */
     KRK_KERNEL_MFMA_LDS = 3, /* bf16 MFMA 16x16x32, W and x rows streamed row-contiguously through LDS */
-    KRK_KERNEL_STREAM = 5   /* persistent bf16 MFMA: W through an LDS DMA ring, x held in registers */
+    KRK_KERNEL_STREAM = 5,  /* persistent bf16 MFMA: W through an LDS DMA ring, x held in registers */
+    KRK_KERNEL_SLICE = 6    /* bf16 MFMA, every wave DMAs its own K chunks of W and x into a private
+                               LDS ring (no barrier in the loop); plain epilogue, M <= 32 */
 };
 
 typedef struct krk_gemm_config {
@@ -113,11 +115,14 @@ typedef struct krk_gemm_config {
                      blocks in flight per row (2, 3, 4, 5, 7, 8, 10, 19, at most 48
                      loads in flight per lane); MFMA_LDS: stages in flight (2, or 3
                      when m_tiles + n_tiles <= 6); STREAM: ring depth in 512-k
-                     stages (2..8, less at large M) */
+                     stages (2..8, less at large M); SLICE: K chunks in flight per
+                     wave (2 or 3) */
     int waves;    /* waves per workgroup (MFMA: 1, 2, 4; VALU: 1 to 8; MFMA_LDS and STREAM: 8) */
     int splits;   /* K partitions across workgroups, reduced in fixed order (1..32) */
     int k_chunk;  /* MFMA_LDS: k per pipeline stage, 256 or 512 (512 needs
-                     m_tiles + n_tiles <= 4); other kernels: ignored */
+                     m_tiles + n_tiles <= 4); SLICE: k per wave chunk, 64 or 128
+                     (128 for up to 16 channels and M <= 16, 2 chunks in
+                     flight); other kernels: ignored */
     int prologue; /* normed calls (krk_gemm_bf16_normed_config): 0 = fused into
                      the projection kernel where the configuration allows it
                      (krk_gemm_normed_fused), else a separate prologue kernel;
@@ -129,8 +134,10 @@ typedef struct krk_gemm_config {
                      kernel and tile width, else all of them).
                      Fewer channels than the tiles hold leave the rest of the
                      last tile as padding (not loaded), so a shape can be cut
-                     into exactly as many blocks as there are CUs.  Other
-                     kernels: ignored. */
+                     into exactly as many blocks as there are CUs.  SLICE:
+                     output channels per workgroup, 1..32 (n_tiles and m_tiles
+                     follow from channels and M); 0 = the plan's, else
+                     N / 256 rounded up.  Other kernels: ignored. */
     int x_preload; /* MFMA_LDS: 1 = x rows loaded with every stage's weight
                      rows; 2 = x rows of the whole K loaded into registers
                      once, before the first stage, so the stage loop loads
@@ -363,12 +370,13 @@ int krk_gemm_bf16_noalloc(const void* x, int64_t ldx,
  * krk_abi_version — KRK_ABI_VERSION of the built library.  The version moves
  *   whenever a declaration or the krk_gemm_config layout changes (version 3:
  *   the ten-int krk_gemm_config above, prologue/channels/x_preload added to
- *   version 1's seven ints).
+ *   version 1's seven ints; version 4: kernel KRK_KERNEL_SLICE, which a
+ *   plan or a candidate list may now name).
  * krk_gemm_config_size — sizeof(krk_gemm_config) in the built library.  A
  *   binding must check both at load time and refuse a mismatch: a config
  *   array of another layout would be over- or under-read.
  */
-#define KRK_ABI_VERSION 3
+#define KRK_ABI_VERSION 4
 int krk_abi_version(void);
 size_t krk_gemm_config_size(void);
 

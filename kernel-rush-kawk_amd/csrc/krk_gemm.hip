@@ -21,6 +21,7 @@
 #include "krk_mfma_lds.h"
 #include "krk_norm.h"
 #include "krk_select.h"
+#include "krk_slice.h"
 #include "krk_stream.h"
 #include "krk_valu.h"
 
@@ -45,6 +46,7 @@ constexpr size_t kLdsBudget = 65536;
 constexpr size_t kLdsReserve = 1024;
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int cdiv_c(int a, int b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 bool valid_epilogue(int e) { return e == KRK_EPILOGUE_NONE || e == KRK_EPILOGUE_SILU_MUL; }
@@ -74,13 +76,42 @@ Geometry geometry(int M, int N, int epilogue, const krk_gemm_config& c) {
         g.cb = c.waves * (silu ? c.n_tiles / 2 : c.n_tiles);  // n_tiles W rows per wave
     } else if (c.kernel == KRK_KERNEL_STREAM) {
         g.cb = silu ? 8 : 16;  // one 16-row tile: 16 channels, or 8 gate + 8 up rows
-    } else if (c.kernel == KRK_KERNEL_MFMA_LDS && c.channels > 0) {
+    } else if ((c.kernel == KRK_KERNEL_MFMA_LDS || c.kernel == KRK_KERNEL_SLICE) && c.channels > 0) {
         g.cb = c.channels;
     } else {
         g.cb = 16 * (silu ? c.n_tiles / 2 : c.n_tiles);
     }
     g.nblocks = cdiv(g.Nout, g.cb);
     return g;
+}
+
+// SLICE: rows a launch may hold (two 16-row x tiles), most channels per
+// block (two weight tiles), and the instantiated variants: k per chunk KC,
+// weight tiles NT, weight / x groups per chunk NGV / XGV (rows of RG =
+// 1024 / (2·KC) each) and chunks in flight per wave D.  128-k chunks serve up
+// to 16 channels and 16 rows with 2 in flight (measured fastest for o and
+// down at M <= 12); 64-k chunks up to 32 of each.  Every wave's ring of D
+// slots of NGV + XGV KB fits the 160 KB of LDS.
+constexpr int kSliceMaxRows = 32;
+constexpr int kSliceMaxChannels = 32;
+constexpr bool slice_inst(int KC, int NT, int NGV, int XGV, int D) {
+    if (KC != 64 && KC != 128) return false;
+    if (D < 2 || D > 3 || XGV < 1 || NGV < 1) return false;
+    if ((size_t)krk::kSliceWaves * D * (NGV + XGV) * krk::kSliceGroup + kLdsReserve > 163840) return false;
+    if (KC == 64) return XGV <= 4 && (NT == 1 ? NGV <= 2 : (NT == 2 && NGV >= 3 && NGV <= 4));
+    return NT == 1 && NGV <= 4 && XGV <= 4 && D == 2;
+}
+struct SliceShape {
+    int NT, NGV, XGV, MT;
+};
+inline SliceShape slice_shape(int KC, int cb, int Mc) {
+    const int rg = krk::slice_rg(KC);
+    SliceShape v;
+    v.NT = cdiv(cb, 16);
+    v.NGV = cdiv(cb, rg);
+    v.XGV = cdiv(Mc, rg);
+    v.MT = cdiv(v.XGV * rg, 16);
+    return v;
 }
 
 // The dispatch table.  Every projection is HBM-bound (arithmetic intensity is
@@ -106,24 +137,28 @@ const TableEntry kTable[] = {
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
     {6144, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 4, 1)},
     {6144, 2560, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
-    // Whole K per block.  M = 5-32: x held in registers for the whole K, 192
-    // blocks of 32 channels, 3 stages in flight (1-11% faster than staging x
-    // with every stage on 256 blocks of 24 at M = 9-32, 3-6% faster than the
-    // VALU kernel at M = 5-8); M = 33-64: 256 blocks of 24 channels, one per
-    // CU, x staged per 256-k stage.
-    {6144, 2560, KRK_EPILOGUE_NONE, 5, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32, 2)},
+    // Whole K per block.  M = 5-24: the wave-sliced kernel on 256 blocks of 24
+    // channels, 64-k chunks, 2 in flight per wave (M = 8: 7.5 against 8.3 us,
+    // M = 20: 8.9 against 9.6 us for the LDS-staged kernel); M = 25-32: x held
+    // in registers for the whole K, 192 blocks of 32 channels, 3 stages in
+    // flight; M = 33-64: 256 blocks of 24 channels, one per CU, x staged per
+    // 256-k stage.
+    {6144, 2560, KRK_EPILOGUE_NONE, 5, 24, kcfg(KRK_KERNEL_SLICE, 0, 2, 0, 1, 64, 24)},
+    {6144, 2560, KRK_EPILOGUE_NONE, 25, 32, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32, 2)},
     {6144, 2560, KRK_EPILOGUE_NONE, 33, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 256, 24)},
     // o_proj 4096 -> 2560
-    // 5-wave workgroups: 256 of 2 rows per wave at M <= 2, 512 of 1 at M = 3-6
+    // 5-wave workgroups: 256 of 2 rows per wave at M <= 2, 512 of 1 at M = 3-4
     {2560, 4096, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 4, 5, 1)},
     {2560, 4096, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 8, 5, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 3, 6, kcfg(KRK_KERNEL_VALU, 1, 4, 5, 1)},
-    {2560, 4096, KRK_EPILOGUE_NONE, 7, 8, kcfg(KRK_KERNEL_VALU, 2, 4, 8, 1)},
-    // M = 9-32: K unsplit on 160 blocks of 16 channels with x held in
-    // registers for all 8 stages (4-11% faster than staging x with every
-    // stage, and than 3 K splits at M = 17-32); above, 3 stages in flight up
-    // to three x tiles, 2 with four (1-5% faster each way)
-    {2560, 4096, KRK_EPILOGUE_NONE, 9, 32, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512, 16, 2)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 4, 5, 1)},
+    // M = 5-32: the wave-sliced kernel on 256 blocks of 10 channels, K
+    // unsplit, 128-k chunks up to M = 12 and 64-k chunks above, 2 in flight
+    // per wave (M = 8: 6.6 against 7.3 us on the VALU kernel; M = 20: 8.2
+    // against 9.2 us with x held in registers on 160 LDS-staged blocks);
+    // above, 3 stages in flight up to three x tiles, 2 with four (1-5%
+    // faster each way)
+    {2560, 4096, KRK_EPILOGUE_NONE, 5, 12, kcfg(KRK_KERNEL_SLICE, 0, 2, 0, 1, 128, 10)},
+    {2560, 4096, KRK_EPILOGUE_NONE, 13, 32, kcfg(KRK_KERNEL_SLICE, 0, 2, 0, 1, 64, 10)},
     {2560, 4096, KRK_EPILOGUE_NONE, 33, 48, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 4096, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3, 256)},
     // gate_up 2560 -> 2 x 9728 with SiLU*mul
@@ -134,13 +169,14 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 5, 1)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 2, 8, 3)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 3, 4, kcfg(KRK_KERNEL_VALU, 1, 4, 5, 1)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 2, 4, 3)},
-    // M = 9-16: K unsplit on 160 blocks of 16 channels with x held in
-    // registers for all 19 stages (7-10% faster than 6 K splits)
-    {2560, 9728, KRK_EPILOGUE_NONE, 9, 16, kcfg(KRK_KERNEL_MFMA_LDS, 1, 3, 0, 1, 512, 16, 2)},
-    {2560, 9728, KRK_EPILOGUE_NONE, 17, 48, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
+    // M = 2-12: the wave-sliced kernel on 256 blocks of 10 channels, K
+    // unsplit, 128-k chunks, 2 in flight per wave (M = 2: 9.9 against 11.1 us
+    // on the VALU kernel; M = 8: 10.8 against 12.9 us); M = 13-24: 128
+    // blocks of 20 channels in 2 K splits, 64-k chunks (2-3% under the
+    // LDS-staged plans)
+    {2560, 9728, KRK_EPILOGUE_NONE, 2, 12, kcfg(KRK_KERNEL_SLICE, 0, 2, 0, 1, 128, 10)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 13, 24, kcfg(KRK_KERNEL_SLICE, 0, 2, 0, 2, 64, 20)},
+    {2560, 9728, KRK_EPILOGUE_NONE, 25, 48, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 3, 256)},
     {2560, 9728, KRK_EPILOGUE_NONE, 49, 64, kcfg(KRK_KERNEL_MFMA_LDS, 2, 2, 0, 3, 256)},
     // lm_head 2560 -> 151936
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 8, 1)},
@@ -231,6 +267,12 @@ void auto_config(int M, int N, int K, int epilogue, krk_gemm_config* c) {
                 c->x_preload = c->x_preload ? c->x_preload : 1;
             }
             if (c->kernel == KRK_KERNEL_STREAM) c->waves = 8;
+            if (c->kernel == KRK_KERNEL_SLICE) {
+                const SliceShape v = slice_shape(c->k_chunk, c->channels, Mc);
+                c->waves = krk::kSliceWaves;
+                c->n_tiles = v.NT;
+                c->m_tiles = v.MT;
+            }
             if (c->kernel == KRK_KERNEL_VALU) {
                 c->m_tiles = valu_mx(Mc);
                 if (!c->unroll) c->unroll = valu_depth(c->m_tiles, c->n_tiles, cdiv(KST, c->splits));
@@ -417,6 +459,36 @@ int resolve_config(int M, int N, int K, int epilogue, const krk_gemm_config* in,
         if (!c.unroll) c.unroll = same_kernel && a.unroll ? a.unroll : maxd;
         if (c.unroll < 2 || c.unroll > maxd)
             return fail(KRK_ERR_UNSUPPORTED, "STREAM depth (unroll) %d not in 2..%d", c.unroll, maxd);
+        *out = c;
+        return KRK_OK;
+    } else if (c.kernel == KRK_KERNEL_SLICE) {
+        if (epilogue != KRK_EPILOGUE_NONE)
+            return fail(KRK_ERR_UNSUPPORTED, "SLICE computes plain projections (no SILU_MUL epilogue)");
+        if (Mc > kSliceMaxRows)
+            return fail(KRK_ERR_UNSUPPORTED, "SLICE handles M <= %d per launch, got %d", kSliceMaxRows, Mc);
+        if (!c.k_chunk) c.k_chunk = same_kernel ? a.k_chunk : 64;
+        if (c.k_chunk != 64 && c.k_chunk != 128)
+            return fail(KRK_ERR_UNSUPPORTED, "SLICE k_chunk=%d not in {64, 128}", c.k_chunk);
+        if (!c.channels) {
+            const int per_cu = cdiv(N, kCuCount);
+            c.channels = same_kernel ? a.channels : (per_cu < kSliceMaxChannels ? per_cu : kSliceMaxChannels);
+        }
+        if (c.channels < 1 || c.channels > kSliceMaxChannels)
+            return fail(KRK_ERR_UNSUPPORTED, "SLICE channels=%d not in 1..%d", c.channels, kSliceMaxChannels);
+        if (!c.unroll) c.unroll = same_kernel ? a.unroll : 2;
+        if (!c.splits) c.splits = same_kernel ? a.splits : 1;
+        c.waves = krk::kSliceWaves;
+        const SliceShape v = slice_shape(c.k_chunk, c.channels, Mc);
+        c.n_tiles = v.NT;
+        c.m_tiles = v.MT;
+        const int nch = cdiv(K, c.k_chunk);
+        if (c.splits < 1 || c.splits > 32 || c.splits > nch)
+            return fail(KRK_ERR_UNSUPPORTED, "SLICE splits=%d not in 1..min(32, %d chunks of %d k)", c.splits, nch,
+                        c.k_chunk);
+        if (!slice_inst(c.k_chunk, v.NT, v.NGV, v.XGV, c.unroll))
+            return fail(KRK_ERR_UNSUPPORTED, "SLICE variant not instantiated: k_chunk=%d, %d channels, %d rows, %d "
+                        "chunks in flight (64-k chunks: up to 32 channels and rows, 2 or 3 in flight within 160 KB "
+                        "of LDS; 128-k chunks: up to 16 of each, 2 in flight)", c.k_chunk, c.channels, Mc, c.unroll);
         *out = c;
         return KRK_OK;
     } else if (c.kernel == KRK_KERNEL_VALU) {
@@ -710,6 +782,69 @@ int dispatch_stream(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, 
         case 4: return xf ? dispatch_stream_xs<4, SILU, true>(a, c, nblocks, s) : dispatch_stream_xs<4, SILU>(a, c, nblocks, s);
     }
     return fail(KRK_ERR_UNSUPPORTED, "STREAM m_tiles=%d", c.m_tiles);
+}
+
+template <int KC, int NT, int NGV, int XGV, int D>
+int launch_slice(const LaunchArgs& a, int nblocks, hipStream_t stream) {
+    constexpr int MT = cdiv_c(XGV * krk::slice_rg(KC), 16);
+    const void* fn = reinterpret_cast<const void*>(&krk::slice_gemm_kernel<MT, NT, D, KC, NGV, XGV>);
+    const size_t shm = krk::slice_lds_bytes(MT, NT, D, NGV, XGV);
+    static std::atomic<uint64_t> done{0};
+    const hipError_t attr = shm > 65536 ? ensure_lds_limit(fn, (int)shm, done) : hipSuccess;
+    if (attr != hipSuccess) return hip_status(attr, "slice_gemm_kernel LDS attribute");
+    // Chunk ranges of the splits, so the kernel divides nothing.
+    const int nch = cdiv(a.K, KC);
+    int cper = nch / a.splits, crem = nch % a.splits, cb = a.cb;
+    void* args[] = {(void*)&a.x, (void*)&a.ldx, (void*)&a.w,      (void*)&a.ldw, (void*)&a.y,    (void*)&a.ldy,
+                    (void*)&a.M, (void*)&a.N,   (void*)&a.K,      (void*)&a.splits, (void*)&cb, (void*)&cper,
+                    (void*)&crem, (void*)&a.part, (void*)&a.ctr};
+    hipError_t e = hipLaunchKernel(fn, dim3(nblocks, a.splits), dim3(64 * krk::kSliceWaves), args, shm, stream);
+    return hip_status(e, "slice_gemm_kernel launch");
+}
+
+template <int KC, int NT, int NGV, int XGV>
+int dispatch_slice_d(const LaunchArgs& a, int D, int nblocks, hipStream_t s) {
+    if (D == 2) {
+        if constexpr (slice_inst(KC, NT, NGV, XGV, 2)) return launch_slice<KC, NT, NGV, XGV, 2>(a, nblocks, s);
+    } else if (D == 3) {
+        if constexpr (slice_inst(KC, NT, NGV, XGV, 3)) return launch_slice<KC, NT, NGV, XGV, 3>(a, nblocks, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "SLICE variant KC=%d NT=%d groups %d+%d D=%d", KC, NT, NGV, XGV, D);
+}
+
+template <int KC, int NT, int NGV>
+int dispatch_slice_x(const LaunchArgs& a, int XGV, int D, int nblocks, hipStream_t s) {
+    switch (XGV) {
+        case 1: return dispatch_slice_d<KC, NT, NGV, 1>(a, D, nblocks, s);
+        case 2: return dispatch_slice_d<KC, NT, NGV, 2>(a, D, nblocks, s);
+        case 3: return dispatch_slice_d<KC, NT, NGV, 3>(a, D, nblocks, s);
+        case 4: return dispatch_slice_d<KC, NT, NGV, 4>(a, D, nblocks, s);
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "SLICE x groups=%d", XGV);
+}
+
+template <int KC>
+int dispatch_slice_kc(const LaunchArgs& a, const SliceShape& v, int D, int nblocks, hipStream_t s) {
+    if (v.NT == 1) {
+        switch (v.NGV) {
+            case 1: return dispatch_slice_x<KC, 1, 1>(a, v.XGV, D, nblocks, s);
+            case 2: return dispatch_slice_x<KC, 1, 2>(a, v.XGV, D, nblocks, s);
+            case 3: return dispatch_slice_x<KC, 1, 3>(a, v.XGV, D, nblocks, s);
+            case 4: return dispatch_slice_x<KC, 1, 4>(a, v.XGV, D, nblocks, s);
+        }
+    } else if (v.NT == 2) {
+        switch (v.NGV) {
+            case 3: return dispatch_slice_x<KC, 2, 3>(a, v.XGV, D, nblocks, s);
+            case 4: return dispatch_slice_x<KC, 2, 4>(a, v.XGV, D, nblocks, s);
+        }
+    }
+    return fail(KRK_ERR_UNSUPPORTED, "SLICE weight tiles=%d groups=%d", v.NT, v.NGV);
+}
+
+int dispatch_slice(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, hipStream_t s) {
+    const SliceShape v = slice_shape(c.k_chunk, a.cb, a.M);
+    return c.k_chunk == 128 ? dispatch_slice_kc<128>(a, v, c.unroll, nblocks, s)
+                            : dispatch_slice_kc<64>(a, v, c.unroll, nblocks, s);
 }
 
 template <int MX, int R, int D, bool SILU, bool NORM = false, bool SEL = false>
@@ -1069,6 +1204,8 @@ int gemm_impl(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, i
             rc = silu ? dispatch_mfma_lds<true>(a, c, g.nblocks, st) : dispatch_mfma_lds<false>(a, c, g.nblocks, st);
         } else if (c.kernel == KRK_KERNEL_STREAM) {
             rc = silu ? dispatch_stream<true>(a, c, g.nblocks, st, xf) : dispatch_stream<false>(a, c, g.nblocks, st, xf);
+        } else if (c.kernel == KRK_KERNEL_SLICE) {
+            rc = dispatch_slice(a, c, g.nblocks, st);
         } else {
             rc = silu ? dispatch_valu<true>(a, c, g.nblocks, st) : dispatch_valu<false>(a, c, g.nblocks, st);
         }
@@ -1116,6 +1253,7 @@ int dispatch_plain(const LaunchArgs& a, const krk_gemm_config& c, int nblocks, h
         case KRK_KERNEL_MFMA: return dispatch_mfma<false>(a, c, nblocks, st);
         case KRK_KERNEL_MFMA_LDS: return dispatch_mfma_lds<false>(a, c, nblocks, st);
         case KRK_KERNEL_STREAM: return dispatch_stream<false>(a, c, nblocks, st);
+        case KRK_KERNEL_SLICE: return dispatch_slice(a, c, nblocks, st);
         default: return dispatch_valu<false>(a, c, nblocks, st);
     }
 }
@@ -1591,6 +1729,16 @@ int krk_gemm_candidates(int M, int N, int K, int epilogue, krk_gemm_config* out,
         for (int sp : wide_splits) add(krk_gemm_config{KRK_KERNEL_STREAM, 0, 0, d, 0, sp, 0});
     for (int nt : nts)
         for (int sp : {1, 2, 4}) add(krk_gemm_config{KRK_KERNEL_MFMA, 0, nt, 4, 4, sp, 0});
+    // SLICE: one block per CU (per CU and split), the same rounded up to 8,
+    // and whole 16-row tiles; 64- and 128-k chunks, 2 or 3 in flight.
+    if (epilogue == KRK_EPILOGUE_NONE && Mc <= kSliceMaxRows)
+        for (int sp : {1, 2})
+            for (int kc : {64, 128})
+                for (int d : {2, 3}) {
+                    const int one = cdiv(N * sp, kCuCount);
+                    for (int ch : {one, cdiv(one, 8) * 8, 16, 32})
+                        add(krk_gemm_config{KRK_KERNEL_SLICE, 0, 0, d, 0, sp, kc, 0, ch, 0});
+                }
     g_err[0] = '\0';  // rejected candidates are not an error of this call
     for (int i = 0; i < n && i < cap; ++i) out[i] = found[i];
     return n;

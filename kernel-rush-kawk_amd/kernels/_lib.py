@@ -32,6 +32,7 @@ KERNEL_MFMA = 1
 KERNEL_VALU = 2
 KERNEL_MFMA_LDS = 3
 KERNEL_STREAM = 5
+KERNEL_SLICE = 6
 
 #: Every function the header declares, with (restype, argtypes).
 _c_void_p = ctypes.c_void_p
@@ -108,7 +109,7 @@ SIGNATURES = {
 }
 
 #: The ABI this binding was written against (KRK_ABI_VERSION in include/krk_gemm.h).
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()

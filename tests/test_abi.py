@@ -58,7 +58,7 @@ def test_binding_refuses_another_abi(monkeypatch):
     from the binding's (here: the binding pretends to expect version 2)."""
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "ABI_VERSION", 2)
-    with pytest.raises(ImportError, match="ABI version 3"):
+    with pytest.raises(ImportError, match=r"ABI version \d+ with a 40-byte"):
         _lib.load()
 
 
@@ -92,8 +92,8 @@ def test_argument_errors(lib, kw, code, msg):
 
 
 def _split_shape(lib):
-    """A shape whose plan splits K (down_proj at M = 8) and its workspace size."""
-    M, N, K = 8, 2560, 9728
+    """A shape whose plan splits K (down_proj at M = 24) and its workspace size."""
+    M, N, K = 24, 2560, 9728
     cfg = GemmConfig()
     assert lib.krk_gemm_plan(M, N, K, NONE, ctypes.byref(cfg)) == 0 and cfg.splits > 1
     need = lib.krk_gemm_workspace_bytes(M, N, K, NONE)
@@ -106,6 +106,8 @@ def _channels_per_block(c, epi):
         return 8 if epi == SILU else 16
     if c["kernel"] == _lib.KERNEL_VALU:
         return c["waves"] * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
+    if c["kernel"] in (_lib.KERNEL_MFMA_LDS, _lib.KERNEL_SLICE) and c["channels"]:
+        return c["channels"]
     return 16 * (c["n_tiles"] // 2 if epi == SILU else c["n_tiles"])
 
 
@@ -154,7 +156,10 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
     cfg = GemmConfig()
     assert lib.krk_gemm_plan(M, N, K, epi, ctypes.byref(cfg)) == 0
     c = cfg.as_dict()
-    assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM, _lib.KERNEL_VALU)
+    assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM, _lib.KERNEL_VALU,
+                           _lib.KERNEL_SLICE)
+    if c["kernel"] == _lib.KERNEL_SLICE:
+        assert M <= 32 and epi == NONE and 1 <= c["channels"] <= 32
     if c["kernel"] == _lib.KERNEL_VALU:
         assert M <= 8 and c["m_tiles"] in (1, 2, 4, 8) and c["m_tiles"] >= M
     else:
@@ -168,22 +173,26 @@ def test_plan_covers_rows_and_fills_the_chip(lib, shape, M):
 
 def test_x_preload_resolution(lib):
     """x_preload resolves to the plan's choice for MFMA_LDS (2 for qkv at
-    M = 5-32 and o at M = 9-32, 1 at 33-64 and where x cannot be held), to 0 for the other
-    kernels, and a caller's 1 or 2 is kept where it is valid."""
+    M = 25-32, 1 at 33-64 and where x cannot be held), to 0 for the other kernels (the wave-sliced
+    plans of qkv at M = 5-24, o at M = 5-32 and down at M = 2-24 among them), and a caller's 1 or 2
+    is kept where it is valid."""
     def resolve(M, N, K, **kw):
         out = GemmConfig()
         assert lib.krk_gemm_resolve(M, N, K, NONE, ctypes.byref(GemmConfig.from_dict(kw)), ctypes.byref(out)) == 0
         return out.as_dict()
-    assert resolve(12, 6144, 2560)["x_preload"] == 2
-    assert resolve(20, 6144, 2560)["x_preload"] == 2
+    assert resolve(12, 6144, 2560)["x_preload"] == 0  # SLICE
+    assert resolve(28, 6144, 2560)["x_preload"] == 2
+    assert resolve(20, 6144, 2560)["x_preload"] == 0  # SLICE
     assert resolve(32, 6144, 2560)["x_preload"] == 2
     assert resolve(33, 6144, 2560)["x_preload"] == 1
     assert resolve(12, 6144, 2560, kernel=3, k_chunk=256)["x_preload"] == 1  # the plan's 2 does not apply
     assert resolve(12, 6144, 2560, kernel=3, x_preload=1)["x_preload"] == 1
     assert resolve(24, 6144, 2560, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2
-    assert resolve(20, 2560, 4096)["x_preload"] == 2  # o: 8 stages of 512 in registers
+    assert resolve(20, 2560, 4096)["x_preload"] == 0  # o: SLICE
+    assert resolve(20, 2560, 4096, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2  # 8 stages
     assert resolve(40, 2560, 4096, kernel=3)["x_preload"] == 1  # three x tiles: staged with every stage
-    assert resolve(12, 2560, 9728)["x_preload"] == 2  # down: 19 stages, one x tile and one weight tile
+    # down: 19 stages, one x tile and one weight tile
+    assert resolve(14, 2560, 9728, kernel=3, n_tiles=1, k_chunk=512, x_preload=2)["x_preload"] == 2
     for nt, ok in ((1, True), (2, False)):
         want = GemmConfig.from_dict(dict(kernel=3, n_tiles=nt, k_chunk=512, splits=1, x_preload=2))
         rc = lib.krk_gemm_resolve(12, 2560, 9728, NONE, ctypes.byref(want), ctypes.byref(GemmConfig()))
@@ -192,7 +201,7 @@ def test_x_preload_resolution(lib):
         want = GemmConfig.from_dict(dict(kernel=3, n_tiles=1, k_chunk=512, x_preload=2))
         rc = lib.krk_gemm_resolve(20, 2560, K, NONE, ctypes.byref(want), ctypes.byref(GemmConfig()))
         assert (rc == 0) == ok, (K, _lib.last_error())
-    for kernel in (1, 2, 5):
+    for kernel in (1, 2, 5, 6):
         assert resolve(8, 6144, 2560, kernel=kernel, x_preload=2)["x_preload"] == 0
 
 
@@ -213,6 +222,11 @@ def test_x_preload_resolution(lib):
     (dict(kernel=3, k_chunk=256, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
     (dict(kernel=3, k_chunk=512, n_tiles=2, splits=2, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
     (dict(kernel=3, m_tiles=3, n_tiles=1, k_chunk=512, x_preload=2), _lib.KRK_ERR_UNSUPPORTED, "x_preload"),
+    (dict(kernel=6, k_chunk=256), _lib.KRK_ERR_UNSUPPORTED, "k_chunk"),
+    (dict(kernel=6, channels=33), _lib.KRK_ERR_UNSUPPORTED, "channels"),
+    (dict(kernel=6, unroll=4), _lib.KRK_ERR_UNSUPPORTED, "not instantiated"),
+    (dict(kernel=6, k_chunk=128), _lib.KRK_ERR_UNSUPPORTED, "not instantiated"),
+    (dict(kernel=6, splits=41), _lib.KRK_ERR_UNSUPPORTED, "splits"),
 ])
 def test_config_errors(lib, cfg, code, msg):
     c = GemmConfig.from_dict(cfg)
@@ -552,12 +566,16 @@ def test_candidates_search_space(lib, M):
         assert len({tuple(sorted(c.items())) for c in cfgs}) == n
         kinds = {c["kernel"] for c in cfgs}
         assert (_lib.KERNEL_VALU in kinds) == (min(M, 64) <= 8)
+        assert (_lib.KERNEL_SLICE in kinds) == (min(M, 64) <= 32 and epi == NONE)
         assert {_lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM} <= kinds
         for c in cfgs:
-            assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_VALU, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM)
+            assert c["kernel"] in (_lib.KERNEL_MFMA, _lib.KERNEL_VALU, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_STREAM,
+                                   _lib.KERNEL_SLICE)
             assert all(c[f] > 0 for f in ("m_tiles", "n_tiles", "unroll", "waves", "splits")), c
             if c["kernel"] == _lib.KERNEL_MFMA_LDS:
                 assert c["k_chunk"] in (256, 512)
+            if c["kernel"] == _lib.KERNEL_SLICE:
+                assert c["k_chunk"] in (64, 128) and c["unroll"] in (2, 3) and c["waves"] == 8
             if epi == SILU and c["kernel"] != _lib.KERNEL_STREAM:
                 assert c["n_tiles"] % 2 == 0, c
             # Each one is accepted again as an explicit configuration.

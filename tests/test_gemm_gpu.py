@@ -289,7 +289,13 @@ SPECIAL_FAMILIES = [
     ("stream", 33, dict(kernel=_lib.KERNEL_STREAM, splits=1)),
     ("stream split-K", 8, dict(kernel=_lib.KERNEL_STREAM, splits=2)),
     ("register mfma split-K", 13, dict(kernel=_lib.KERNEL_MFMA, splits=2)),
+    ("wave-sliced", 8, dict(kernel=_lib.KERNEL_SLICE, channels=10, splits=1)),
+    ("wave-sliced 128-k chunks", 12, dict(kernel=_lib.KERNEL_SLICE, k_chunk=128, channels=13, splits=1)),
+    ("wave-sliced split-K", 20, dict(kernel=_lib.KERNEL_SLICE, channels=24, splits=3)),
 ]
+# The wave-sliced kernel computes plain projections only.
+SPECIAL_CASES = [(f, M, c, epi) for f, M, c in SPECIAL_FAMILIES for epi in (NONE, SILU)
+                 if not (epi == SILU and c["kernel"] == _lib.KERNEL_SLICE)]
 
 
 # (a, b) pairs whose fp32 sum a + b is exact and lies exactly halfway between
@@ -366,8 +372,8 @@ def _assert_special_parity(y, ref, what):
     assert not bad.any(), f"{what}: {int(bad.sum())} finite values outside 2e-2 + 1e-2|ref|"
 
 
-@pytest.mark.parametrize("family,M,config", SPECIAL_FAMILIES, ids=[f[0] for f in SPECIAL_FAMILIES])
-@pytest.mark.parametrize("epi", [NONE, SILU], ids=["plain", "silu_mul"])
+@pytest.mark.parametrize("family,M,config,epi", SPECIAL_CASES,
+                         ids=[f"{c[0]}-{'plain' if c[3] == NONE else 'silu_mul'}" for c in SPECIAL_CASES])
 def test_special_values_propagate(device, family, M, config, epi):
     """NaN, +-inf and -0 in x and in W rows, through every kernel family
     (VALU dot2, LDS-staged MFMA, stream MFMA, register MFMA), the split-K
@@ -551,7 +557,7 @@ def test_lds_x_in_registers_configs(device, M, N, K, epi):
     _run_configs(x, w, epi, _lds_xpre_configs(M, epi == SILU))
 
 
-@pytest.mark.parametrize("kernel", [_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_VALU])
+@pytest.mark.parametrize("kernel", [_lib.KERNEL_MFMA, _lib.KERNEL_MFMA_LDS, _lib.KERNEL_VALU, _lib.KERNEL_SLICE])
 @pytest.mark.parametrize("splits", [8, 9, 16, 17, 32])
 def test_many_splits_fixed_order(device, kernel, splits):
     """Split counts around and past the fix-up's load batch (8 splits per round
@@ -574,6 +580,27 @@ def test_all_stream_configs_agree(device, M, N, K):
     x = R.randn_bf16((M, K), 8800 + M)
     w = R.randn_bf16((N, K), 8801 + N, 0.02)
     _run_configs(x, w, NONE, _stream_configs(M, K))
+
+
+def _slice_configs(M):
+    """Wave-sliced configurations: 64- and 128-k chunks, 2 or 3 in flight,
+    channel counts from one to two full tiles (partial 8- and 4-row groups),
+    K unsplit and split (more splits than some waves have chunks)."""
+    for kc, d, ch, sp in itertools.product((64, 128), (2, 3), (1, 5, 8, 10, 13, 16, 17, 24, 32), (1, 2, 7)):
+        yield dict(kernel=_lib.KERNEL_SLICE, k_chunk=kc, unroll=d, channels=ch, splits=sp)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 96, 1536), (5, 200, 1000), (8, 2560, 4096), (13, 33, 2568), (16, 130, 8),
+                                   (24, 6144, 520), (32, 97, 1096), (9, 2560, 9728)])
+def test_all_slice_configs_agree(device, M, N, K):
+    """The wave-sliced kernel under every instantiated variant: ragged K (a
+    tail chunk with its pieces past K masked, and K below one chunk), N that
+    is not a multiple of the block's channels (its last block loads clamped
+    rows it does not store), M that leaves a partial x group, and split K,
+    against the oracle and within the fp32 bound."""
+    x = R.randn_bf16((M, K), 8850 + M)
+    w = R.randn_bf16((N, K), 8851 + N, 0.02)
+    _run_configs(x, w, NONE, _slice_configs(M))
 
 
 @pytest.mark.parametrize("M,I,K", [(1, 40, 1536), (8, 52, 1000), (33, 24, 2568), (64, 100, 520)])

@@ -93,10 +93,10 @@ def test_first_call_captured_in_a_graph(device):
             say("eager o M=48 between replays")
             eager = noalloc(xo, wo, torch.empty((48, O[1]), dtype=torch.bfloat16, device=device), NONE)
             assert torch.equal(eager, with_workspace(xo, wo, NONE))
-            xd, wd = operands(8, DOWN, 9820, device)
-            assert splits(8, DOWN) > 1
-            say("eager down M=8 between replays")
-            eager = noalloc(xd, wd, torch.empty((8, DOWN[1]), dtype=torch.bfloat16, device=device), NONE)
+            xd, wd = operands(24, DOWN, 9820, device)
+            assert splits(24, DOWN) > 1
+            say("eager down M=24 between replays")
+            eager = noalloc(xd, wd, torch.empty((24, DOWN[1]), dtype=torch.bfloat16, device=device), NONE)
             assert torch.equal(eager, with_workspace(xd, wd, NONE))
         say("replay", rep)
         g.replay()
@@ -107,7 +107,7 @@ def test_first_call_captured_in_a_graph(device):
 
 # (name, epilogue, shape, first M, second M, whether both plans split K)
 PAIRS = [
-    ("down, split K at both sizes", NONE, DOWN, 64, 8, True),
+    ("down, split K at both sizes", NONE, DOWN, 64, 24, True),
     ("o, split K at both sizes", NONE, O, 64, 48, True),
     ("o, split K then unsplit", NONE, O, 48, 8, False),
     ("gate_up + SiLU*mul", SILU, GATE_UP, 16, 3, False),
@@ -136,11 +136,11 @@ def test_noalloc_matches_workspace_entry_point(device, name, epi, shape, M1, M2,
 
 def test_split_k_repeats_bit_exact_through_the_python_wrapper(device):
     """The scratch keeps the last call's contents: every split-K call must
-    leave the shared counters at zero, so down_proj at M = 8 (3 K splits)
+    leave the shared counters at zero, so down_proj at M = 24 (3 K splits)
     repeats bit-identically with a split-K o_proj call of another shape in
     between.  The calls go through kernels.gemm.gemm_noalloc."""
-    assert splits(8, DOWN) > 1 and splits(64, O) > 1
-    x, w = operands(8, DOWN, 9950, device)
+    assert splits(24, DOWN) > 1 and splits(64, O) > 1
+    x, w = operands(24, DOWN, 9950, device)
     xo, wo = operands(64, O, 9960, device)
     want = with_workspace(x, w, NONE)
     want_o = with_workspace(xo, wo, NONE)
@@ -148,7 +148,7 @@ def test_split_k_repeats_bit_exact_through_the_python_wrapper(device):
         say("repeat", rep)
         got = G.gemm_noalloc(x, w, torch.full_like(want, float("nan")))
         torch.cuda.synchronize()
-        assert torch.equal(got, want), f"repeat {rep}: down M=8 differs"
+        assert torch.equal(got, want), f"repeat {rep}: down M=24 differs"
         got_o = G.gemm_noalloc(xo, wo, torch.full_like(want_o, float("nan")))
         torch.cuda.synchronize()
         assert torch.equal(got_o, want_o), f"repeat {rep}: o M=64 differs"
