@@ -21,7 +21,9 @@
 //     every stage of the workgroup's K range — so x costs one L2 read per CU
 //     instead of one per block, and no load in the loop competes with the
 //     ring in the in-order vmcnt counter.  It is read as whole 1 KB row
-//     pieces and turned into fragments through LDS before the ring starts.
+//     pieces and turned into fragments through LDS before the ring starts
+//     (one 16-row tile: 8 rows x 128 B per load, fragments formed in
+//     registers).
 //   * Waits are explicit (vmcnt = DMAs issued after the consumed stage) and
 //     barriers carry no memory fence, so the compiler never drains the ring.
 //
@@ -176,55 +178,91 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         for (int d = 0; d < depth - 1 && d < T; ++d) issue(d);
     } else {
-        // x for the workgroup's K range, loaded once.  Whole 1 KB row pieces (wave
-        // w loads rows w, w + 8, ... of every stage): a CU pulls L2 data ~2.5x
-        // faster this way than in the MFMA fragment pattern.  Rows past M, k past
-        // K and stages past the split's range are zero.
-        constexpr int LX = 2 * MT;  // 16·MT rows over 8 waves
-        u32x4 XR[XS][LX];
+        if constexpr (MT == 1) {
+            // One 16-row tile: each wave loads only its own 128 bytes of every
+            // row (k-steps KPW·w, KPW·w + 1 of each stage), as two loads of 8
+            // rows x 128 B (whole lines): lane (q, b3, rho) of load h gets row
+            // 8h + rho, 16-byte piece 4·(b3 ^ h) + q.  Fragment kk = 0 (pieces
+            // 0-3) is load b3 taken lane by lane; kk = 1 (pieces 4-7) is load
+            // 1 - b3 moved by 8 lanes within each 16-lane row (DPP row_ror:8).
+            // No LDS trip and no barrier (measured: gate_up at M = 9-16 0.3-0.75
+            // us faster, output bit-identical; with two or more tiles the 8-row
+            // loads ingest more slowly than whole row pieces, 1.7-4.2 us slower).
+            // Rows past M, k past K and stages past the split's range are zero.
+            static_assert(KPW == 2, "two k-steps (128 bytes) per wave per stage");
+            const int b3 = (lane >> 3) & 1;
+            const int rho = lane & 7;
+            u32x4 V[XS][2];
 #pragma unroll
-        for (int j = 0; j < XS; ++j) {
-            const int k = (sb + j) * kStreamKC + klane;
-            const bool kok = j < nst && k < K;
+            for (int j = 0; j < XS; ++j)
 #pragma unroll
-            for (int i = 0; i < LX; ++i) {
-                const int m = wave + WV * i;
-                const u32x4 v = load_cached16(x + (int64_t)(m < M ? m : M - 1) * ldx + (kok ? k : 0));
-                XR[j][i] = (kok && m < M) ? v : u32x4{0u, 0u, 0u, 0u};
+                for (int h = 0; h < 2; ++h) {
+                    const int m = 8 * h + rho;
+                    const int k = (sb + j) * kStreamKC + 32 * KPW * wave + 8 * (4 * (b3 ^ h) + q);
+                    const bool kok = j < nst && k < K;
+                    const u32x4 v = load_cached16(x + (int64_t)(m < M ? m : M - 1) * ldx + (kok ? k : 0));
+                    V[j][h] = (kok && m < M) ? v : u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+            for (int j = 0; j < XS; ++j) {
+                X[j][0][0] = b3 ? V[j][1] : V[j][0];
+                const u32x4 yv = b3 ? V[j][0] : V[j][1];
+                constexpr int kRowRor8 = 0x128;  // DPP row_ror:8
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    X[j][1][0][e] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)yv[e], kRowRor8, 0xF, 0xF, false);
             }
-        }
-        // The rows go through LDS (16·MT rows of 1 KB per stage, up to XG
-        // stages at a time from the start of the area, idle until the ring
-        // starts and the first block ends; chunks XOR-swizzled by row so the
-        // fragment reads hit distinct banks) and come back as this wave's MFMA
-        // fragments X[j][kk][i]: one write, barrier, read, barrier round per
-        // group of XG stages.
-        constexpr int XG = stream_xgroup(MT);
-        unsigned char* const xstage = smem;
+        } else {
+            // x for the workgroup's K range, loaded once.  Whole 1 KB row pieces (wave
+            // w loads rows w, w + 8, ... of every stage): a CU pulls L2 data ~2.5x
+            // faster this way than in the MFMA fragment pattern.  Rows past M, k past
+            // K and stages past the split's range are zero.
+            constexpr int LX = 2 * MT;  // 16·MT rows over 8 waves
+            u32x4 XR[XS][LX];
 #pragma unroll
-        for (int j0 = 0; j0 < XS; j0 += XG) {
-#pragma unroll
-            for (int j = j0; j < j0 + XG && j < XS; ++j)
+            for (int j = 0; j < XS; ++j) {
+                const int k = (sb + j) * kStreamKC + klane;
+                const bool kok = j < nst && k < K;
 #pragma unroll
                 for (int i = 0; i < LX; ++i) {
                     const int m = wave + WV * i;
-                    *reinterpret_cast<u32x4*>(xstage + (j - j0) * kStreamXStageBytes * MT + m * 1024 +
-                                              16 * (lane ^ (m & 15))) = XR[j][i];
+                    const u32x4 v = load_cached16(x + (int64_t)(m < M ? m : M - 1) * ldx + (kok ? k : 0));
+                    XR[j][i] = (kok && m < M) ? v : u32x4{0u, 0u, 0u, 0u};
                 }
-            lds_wait();
-            bare_barrier();
+            }
+            // The rows go through LDS (16·MT rows of 1 KB per stage, up to XG
+            // stages at a time from the start of the area, idle until the ring
+            // starts and the first block ends; chunks XOR-swizzled by row so the
+            // fragment reads hit distinct banks) and come back as this wave's MFMA
+            // fragments X[j][kk][i]: one write, barrier, read, barrier round per
+            // group of XG stages.
+            constexpr int XG = stream_xgroup(MT);
+            unsigned char* const xstage = smem;
 #pragma unroll
-            for (int j = j0; j < j0 + XG && j < XS; ++j)
+            for (int j0 = 0; j0 < XS; j0 += XG) {
 #pragma unroll
-                for (int kk = 0; kk < KPW; ++kk) {
-                    const int c = 4 * (wave * KPW + kk) + q;
+                for (int j = j0; j < j0 + XG && j < XS; ++j)
 #pragma unroll
-                    for (int i = 0; i < MT; ++i)
-                        X[j][kk][i] = *reinterpret_cast<const u32x4*>(xstage + (j - j0) * kStreamXStageBytes * MT +
-                                                                      (16 * i + r) * 1024 + 16 * (c ^ r));
-                }
-            lds_wait();
-            bare_barrier();
+                    for (int i = 0; i < LX; ++i) {
+                        const int m = wave + WV * i;
+                        *reinterpret_cast<u32x4*>(xstage + (j - j0) * kStreamXStageBytes * MT + m * 1024 +
+                                                  16 * (lane ^ (m & 15))) = XR[j][i];
+                    }
+                lds_wait();
+                bare_barrier();
+#pragma unroll
+                for (int j = j0; j < j0 + XG && j < XS; ++j)
+#pragma unroll
+                    for (int kk = 0; kk < KPW; ++kk) {
+                        const int c = 4 * (wave * KPW + kk) + q;
+#pragma unroll
+                        for (int i = 0; i < MT; ++i)
+                            X[j][kk][i] = *reinterpret_cast<const u32x4*>(xstage + (j - j0) * kStreamXStageBytes * MT +
+                                                                          (16 * i + r) * 1024 + 16 * (c ^ r));
+                    }
+                lds_wait();
+                bare_barrier();
+            }
         }
         // The weight ring starts only now.  Measured: with its prologue in flight
         // the first-touch HBM fills of x queue behind 256 workgroups' worth of
