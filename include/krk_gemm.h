@@ -265,8 +265,8 @@ size_t krk_gemm_normed_workspace_bytes(int M, int N, int K, int epilogue, const 
 int krk_gemm_normed_fused(int M, int N, int K, int epilogue, const krk_gemm_config* cfg);
 
 /* The configuration krk_gemm_bf16_normed uses (the normed plan): fused where
- * that measured fastest (qkv at M <= 16: VALU to M = 4, MFMA_LDS at 5-16;
- * gate_up and lm_head at M <= 2 of Qwen3-4B), else the plain plan with
+ * that measured fastest (qkv at M <= 4, gate_up and lm_head at M <= 2 of
+ * Qwen3-4B, all on the VALU kernel), else the plain plan with
  * prologue = 1.  Like krk_gemm_plan it
  * replaces the configuration pick_normed settles on
  * (engine/kernels/gemm.py:501-560).  KRK_OK or a negative code. */

@@ -1007,11 +1007,10 @@ bool norm_fused(int M, int N, int K, int epilogue, const krk_gemm_config& c) {
 // measured fastest (tuner, graph replay over rotating weights, MI355X); every
 // other shape and M runs its plain plan behind the prologue kernel.
 const TableEntry kNormTable[] = {
-    // qkv: 256 workgroups of 6 waves x 4 rows; at M = 5-16 the LDS-staged
-    // kernel's fused form on 192 blocks of 32 channels (7-12% under the
-    // prologue kernel + plain plan)
+    // qkv: 256 workgroups of 6 waves x 4 rows.  From M = 5 the prologue
+    // kernel + the wave-sliced plain plan (0.1-0.4 us under the LDS-staged
+    // kernel's fused form at M = 6-16, even at M = 5, in four runs).
     {6144, 2560, KRK_EPILOGUE_NONE, 1, 4, kcfg(KRK_KERNEL_VALU, 4, 5, 6, 1)},
-    {6144, 2560, KRK_EPILOGUE_NONE, 5, 16, kcfg(KRK_KERNEL_MFMA_LDS, 2, 3, 0, 1, 512, 32)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 5, 8, 1)},
     {151936, 2560, KRK_EPILOGUE_NONE, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 5, 8, 1)},

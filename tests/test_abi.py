@@ -337,16 +337,15 @@ def test_normed_argument_errors(lib, kw, code, msg):
 
 def test_normed_fused_plans(lib):
     """The normed plans fuse the prologue where that measured fastest (qkv
-    at M <= 16: VALU to M = 4, LDS-staged MFMA at 5-16; gate_up and lm_head
-    at M <= 2) and
+    at M <= 4, gate_up and lm_head at M <= 2, on the VALU kernel) and
     otherwise run the plain plan behind the separate prologue kernel
     (prologue = 1).  A VALU configuration fuses when K is unsplit, the depth
     covers K = 2560 and there is a wave per 512-k block; an LDS-staged one
     when K is unsplit in at most five 512-k stages with one or two x tiles
     and one or two weight tiles; prologue = 1, split K, the stream and the
     register MFMA kernels never fuse."""
-    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["qkv"], 4, 1), (QWEN["qkv"], 8, 1),
-                                  (QWEN["qkv"], 16, 1), (QWEN["qkv"], 17, 0),
+    for (N, K, epi), M, fused in [(QWEN["qkv"], 1, 1), (QWEN["qkv"], 4, 1), (QWEN["qkv"], 5, 0),
+                                  (QWEN["qkv"], 8, 0), (QWEN["qkv"], 16, 0), (QWEN["qkv"], 17, 0),
                                   (QWEN["gate_up"], 1, 1), (QWEN["gate_up"], 2, 1), (QWEN["gate_up"], 8, 0),
                                   (QWEN["lm_head"], 1, 1), (QWEN["lm_head"], 2, 1), (QWEN["lm_head"], 4, 0),
                                   (QWEN["gate_up"], 32, 0), (QWEN["qkv"], 32, 0), (QWEN["lm_head"], 64, 0)]:

@@ -923,7 +923,7 @@ def test_normed_fused_and_prologue_paths_agree(device, M, N, K, epi):
     assert ran >= 3
 
 
-@pytest.mark.parametrize("shape,M", [("qkv", M) for M in (1, 2, 3, 4, 5, 8, 12, 16)] + [("gate_up", M) for M in (1, 2)] +
+@pytest.mark.parametrize("shape,M", [("qkv", M) for M in (1, 2, 3, 4)] + [("gate_up", M) for M in (1, 2)] +
                                     [("lm_head", M) for M in (1, 2)])
 def test_normed_fused_plans_and_separate_prologue(device, shape, M):
     """Normed plans that fuse the prologue (one launch) and the same
