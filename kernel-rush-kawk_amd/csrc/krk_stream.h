@@ -16,9 +16,10 @@
 //     16 rows x 512 k, depth-1 of them in flight while one is consumed, and
 //     it keeps streaming across block boundaries.
 //   * Workgroups are persistent (at most one per CU): workgroup g walks blocks
-//     g, g + G, ...  x is loaded once per workgroup into VGPRs — wave w keeps
-//     the fragments of its fixed share of k-steps (2 of every stage's 16) for
-//     every stage of the workgroup's K range — so x costs one L2 read per CU
+//     g', g' + G, ... (g' its XCD-aware index, below).  x is loaded once per
+//     workgroup into VGPRs — wave w keeps the fragments of its fixed share of
+//     k-steps (2 of every stage's 16) for every stage of the workgroup's K
+//     range — so x costs one L2 read per CU
 //     instead of one per block, and no load in the loop competes with the
 //     ring in the in-order vmcnt counter.  It is read as whole 1 KB row
 //     pieces and turned into fragments through LDS before the ring starts
@@ -116,7 +117,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int r = lane & 15;
     const int q = lane >> 4;
 
-    // This workgroup's split and blocks: blocks gi, gi + Gs, ... of split s.
+    // This workgroup's split and blocks: blocks vg, vg + Gs, ... of split s.
     const int s = blockIdx.x % splits;
     const int gi = blockIdx.x / splits;
     const int Gs = gridDim.x / splits;
@@ -126,7 +127,15 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int sb = (int)(((int64_t)s * KST) / splits);
     const int se = (int)(((int64_t)(s + 1) * KST) / splits);
     const int nst = se - sb;
-    const int myblocks = gi < nblocks ? (nblocks - 1 - gi) / Gs + 1 : 0;
+    // XCD-aware order: workgroups go to the 8 XCDs round robin, so with K
+    // unsplit the workgroups of one XCD (gi = x, x + 8, ...) take adjacent
+    // blocks of each round, vg = x·Gs/8 + gi/8.  The partial lines of y that
+    // neighbouring blocks write then meet in one XCD's L2 instead of being
+    // written back from several.  Measured (bit-identical output): gate_up
+    // at M = 16-64 0.4-0.9 us faster (M = 32: 22.57 -> 21.93 us), lm_head at
+    // M = 32 / 64 4.3 / 6.2 us faster; M = 5-9 within 0.4 us.
+    const int vg = (splits == 1 && (Gs & 7) == 0) ? (gi & 7) * (Gs >> 3) + (gi >> 3) : gi;
+    const int myblocks = vg < nblocks ? (nblocks - 1 - vg) / Gs + 1 : 0;
     const int T = myblocks * nst;  // stages this workgroup consumes
 
     // DMA of the workgroup's t-th stage into ring slot t % depth.
@@ -134,7 +143,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     auto issue = [&](int t) {
         const int bi = t / nst;
         const int st = sb + (t - bi * nst);
-        const int b = gi + bi * Gs;
+        const int b = vg + bi * Gs;
         unsigned char* slot = ring + (size_t)(t % depth) * kStreamSlot;
         const int k = st * kStreamKC + klane;
         const int kc = k < K ? k : 0;  // past K: any in-range address, masked at use
@@ -288,7 +297,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             const int rest = it / CPR;
             const int m = rest % M;
             const int sl = rest / M;
-            const int c0 = (gi + (base + sl) * Gs) * CB + 8 * ch;
+            const int c0 = (vg + (base + sl) * Gs) * CB + 8 * ch;
             const u32x4 v = *reinterpret_cast<const u32x4*>(ob + ((size_t)(sl * MP + m) * CB + 8 * ch));
             uint16_t* dst = y + (int64_t)m * ldy + c0;
             if (vec_ok && c0 + 8 <= Nout) {
@@ -317,7 +326,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     // works.  Partial layout: rb[wave][m tile][lane] f32x4, lane (r, q) holds
     // rows 4q..4q+3 of channel r.
     auto finish_block = [&](int bl, const f32x4* rb) {
-        const int b = gi + bl * Gs;
+        const int b = vg + bl * Gs;
         const int sl = obcap > 0 ? bl % obcap : 0;
         if (splits == 1 && sl == 0 && bl > 0 && (!SEL || y)) {
             // Buffer full: write it out before slot 0 is reused.
