@@ -117,6 +117,11 @@ constexpr int log2_exact() {
 __device__ __forceinline__ u32x4 load_stream16(const uint16_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
+// Block index i of n with each XCD's blocks adjacent (workgroups go to the 8
+// XCDs round robin): XCD x = i mod 8 gets blocks [x·n/8, (x+1)·n/8).  The
+// identity unless 8 divides n.
+__device__ __forceinline__ int xcd_block(int i, int n) { return (n & 7) == 0 ? (i & 7) * (n >> 3) + (i >> 3) : i; }
+
 __device__ __forceinline__ u32x4 load_cached16(const uint16_t* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
