@@ -408,14 +408,14 @@ def _time(fn, iters: int = 30, rotate: list | None = None) -> float:
     return timing.replay_ms(timing.rotation_calls(fn, iters, rotate))
 
 
-def _validate(out: torch.Tensor, ref: torch.Tensor, what: str, log=None) -> None:
-    """The tuner's acceptance (:func:`kernels.tune.close_ok`): every element
-    within ``2e-2 + 1e-2·|ref|`` and the reference's rule
-    (engine/kernels/gemm.py:441-447), max error within ``0.02 * max|ref| + 1e-3``.
-    A failure raises instead of falling back."""
+def _validate(out: torch.Tensor, ref: torch.Tensor, what: str, log=None, silu: bool = False) -> None:
+    """The tuner's acceptance (:func:`kernels.tune.close_ok`, ``silu`` for a
+    SiLU·mul output): every element within ``2e-2 + 1e-2·|ref|`` and the
+    reference's rule (engine/kernels/gemm.py:441-447), max error within
+    ``0.02 * max|ref| + 1e-3``.  A failure raises instead of falling back."""
     from . import tune
 
-    ok, why = tune.close_ok(out, ref)
+    ok, why = tune.close_ok(out, ref, silu)
     if not ok:
         raise RuntimeError(f"{what}: HIP GEMM disagrees with F.linear ({why})")
     if log:
@@ -513,7 +513,7 @@ def tune_projection(a: torch.Tensor, w: torch.Tensor, epilogue: int = EPILOGUE_N
     downs = _down_for(checks, w, rot, down) if strict else []
 
     def judge(out, ref, i=0):
-        ok, why = tune.close_ok(out, ref)
+        ok, why = tune.close_ok(out, ref, epilogue == EPILOGUE_SILU_MUL)
         if ok and strict:
             ok, why = tune.pointwise_ok(out, ref)
         if ok and downs:
@@ -600,7 +600,7 @@ def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = 
     I = wgu.shape[0] // 2
     cfg = tune_projection(a, wgu, EPILOGUE_SILU_MUL, ws, log, cache, down=down).config if tune else None
     mm = SkinnyGateUp(M, I, K, a.device, config=cfg)
-    _validate(mm(a, wgu), _silu_mul(_linear_fp32acc(a, wgu)), f"gateup M={M} I={I} K={K}", log)
+    _validate(mm(a, wgu), _silu_mul(_linear_fp32acc(a, wgu)), f"gateup M={M} I={I} K={K}", log, silu=True)
     if log:
         ms = _time(lambda w_: mm(a, w_), rotate=ws or [wgu])
         log(f"gateup M={M} I={I} K={K}: krk{mm.resolved_config} {ms * 1000:.1f}us "
@@ -645,7 +645,7 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
         ref = _silu_mul(ref)
     if not torch.equal(xout, ref_xout):
         raise RuntimeError(f"normed {kind} M={M} N={N} K={K}: xout differs from x + y")
-    _validate(out, ref, f"normed {kind} M={M} N={N} K={K}", log)
+    _validate(out, ref, f"normed {kind} M={M} N={N} K={K}", log, silu=kind == "gateup")
     if log:
         ms = _time(lambda w_: fn(x, y, w_norm, xout, w_), rotate=ws or [w])
         fused = "fused" if normed_fused(M, N, K, mm.epilogue, cfg) else "prologue kernel"

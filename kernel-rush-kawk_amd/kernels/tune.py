@@ -12,7 +12,8 @@ as a graph replay over every layer's copy of the weight
   dispatch table's choice first, so the table's plan is always the incumbent;
 * a candidate is accepted (:func:`close_ok`) when, on two weights of the
   rotation, every output element is within ``2e-2 + 1e-2 * |ref|`` of an
-  fp32-accumulated torch GEMM and the reference's own rule, max error within
+  fp32-accumulated torch GEMM (a SiLU·mul output's also within the
+  reference's gate/up rule ``0.02 * |ref| + 1e-3``) and the reference's own rule, max error within
   ``0.02 * max|ref| + 1e-3`` (gemm.py:441-447), holds too; for normed
   projections xout must also equal x + y bit for bit (gemm.py:548).  A
   rejected candidate is logged and skipped (it would be a kernel bug: every
@@ -166,13 +167,22 @@ def confirm_ratios(plan_fn, cand_fn, timer, rot) -> tuple[float, float] | None:
     return ratios[0], ratios[1]
 
 
-def close_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
+def close_ok(out: torch.Tensor, ref: torch.Tensor, silu: bool = False) -> tuple[bool, str]:
     """Acceptance of one candidate output against the fp32-accumulated torch
     reference.  Two rules, both required:
 
     * elementwise, the bar this library is held to:
       ``|out - ref| <= 2e-2 + 1e-2 * |ref|`` at every element, with NaN
-      exactly where the reference has NaN and infinities equal;
+      exactly where the reference has NaN and infinities equal.  For a
+      SiLU·mul output (``silu``) an element may instead meet the reference's
+      own gate/up rule ``0.02 * |ref| + 1e-3``
+      (engine/kernels/m64_gateup_selection.py:71-97), which is looser for
+      ``|ref| > ~1.9``: the three bf16 roundings of the epilogue turn a gate
+      or up sum that lands on the other side of a rounding midpoint than
+      torch's (the two fp32 summation orders differ) into a few ulps of the
+      product.  Seen on an MI355X: gate 2.0078133 (exact), 8e-7 above the
+      midpoint of 2 and 2.015625, rounded up by the kernel and down by torch,
+      gave 6.719 against 6.625;
     * globally, the reference's own picker rule (engine/kernels/gemm.py:441-447):
       ``max|out - ref| <= 0.02 * max|ref| + 1e-3`` over the finite elements.
     """
@@ -190,9 +200,13 @@ def close_ok(out: torch.Tensor, ref: torch.Tensor) -> tuple[bool, str]:
     if o.numel() == 0:
         return True, "no finite elements"
     err = (o - r).abs()
-    bad = int((err > 2e-2 + 1e-2 * r.abs()).sum())
+    bar = 2e-2 + 1e-2 * r.abs()
+    if silu:
+        bar = torch.maximum(bar, 0.02 * r.abs() + 1e-3)
+    bad = int((err > bar).sum())
     if bad:
-        return False, f"{bad} elements outside 2e-2 + 1e-2*|ref| (max err {err.max().item():.4g})"
+        rule = "max(2e-2 + 1e-2*|ref|, 0.02*|ref| + 1e-3)" if silu else "2e-2 + 1e-2*|ref|"
+        return False, f"{bad} elements outside {rule} (max err {err.max().item():.4g})"
     worst = err.max().item()
     tol = 0.02 * r.abs().max().item() + 1e-3
     if not worst <= tol:
