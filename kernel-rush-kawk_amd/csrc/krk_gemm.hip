@@ -699,8 +699,15 @@ template <int MT, int XS, bool SILU, int SK = 0, bool XF = false>
 int launch_stream(const LaunchArgs& a, int nblocks, int depth, hipStream_t stream, krk::SelectArgs sa = {}) {
     const void* fn = reinterpret_cast<const void*>(&krk::stream_gemm_kernel<MT, XS, SILU, SK, XF>);
     int nred = stream_nred_for(a.K, a.splits);
-    size_t shm = krk::stream_lds_bytes(MT, depth, nred);
     const int G = stream_groups(nblocks, a.splits);
+    // Two or more x tiles: a second reduction area when it fits beside the
+    // ring and every output block (the kernel then needs no barrier at a
+    // block's second stage).
+    if (MT >= 2 && nred == 1) {
+        const size_t out = a.splits == 1 ? (size_t)cdiv(nblocks, G) * krk::stream_out_bytes(MT, SILU) : 0;
+        if (krk::stream_lds_bytes(MT, depth, 2) + out <= kLdsMax) nred = 2;
+    }
+    size_t shm = krk::stream_lds_bytes(MT, depth, nred);
     // Unsplit K: the rest of the LDS holds finished blocks until the end.
     int obcap = 0;
     if (a.splits == 1) {

@@ -8,10 +8,10 @@
 // pairs 8 gate rows with the matching 8 up rows inside one 16-row tile.
 //
 // Design (each point measured on MI355X):
-//   * HBM3E streams at ~6.5 TB/s only when each wave-wide load is a long
-//     contiguous run: every W load is a 1 KB row chunk (64 lanes x 16 B),
-//     DMA'd straight into LDS (global_load_lds_dwordx4).  MFMA B fragments
-//     are then read from LDS.
+//   * W is DMA'd straight into LDS in whole 128-byte lines
+//     (global_load_lds_dwordx4, 64 lanes x 16 B): with one 16-row x tile as
+//     1 KB row chunks, with more tiles as 8 rows x 128 B of the loading
+//     wave's own k range (below).  MFMA B fragments are then read from LDS.
 //   * A CU needs ~100 KB in flight: the ring holds `depth` stages of
 //     16 rows x 512 k, depth-1 of them in flight while one is consumed, and
 //     it keeps streaming across block boundaries.
@@ -56,7 +56,10 @@ constexpr int kStreamMaxDepth = 8;
 // suffices (the next block parks its sums only after its second stage's
 // barrier, which every wave reaches after that reduction); with one stage
 // per block the blocks alternate between two.  The area saved goes to the
-// ring (measured: at 64 rows two areas left room for only 4 stages).
+// ring (measured: at 64 rows two areas left room for only 4 stages).  With
+// two or more x tiles the launch takes two areas whenever they fit beside
+// the ring and every output block, so that only a block's first stage ends
+// in a barrier.
 __host__ __device__ constexpr size_t stream_red_bytes(int MT) { return (size_t)kStreamWaves * MT * 64 * 16; }
 __host__ __device__ constexpr int stream_nred(int stages_per_split) { return stages_per_split >= 2 ? 1 : 2; }
 __host__ __device__ constexpr size_t stream_lds_bytes(int MT, int depth, int nred) {
@@ -139,17 +142,34 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
     const int T = myblocks * nst;  // stages this workgroup consumes
 
     // DMA of the workgroup's t-th stage into ring slot t % depth.
+    //   * One 16-row x tile: wave w loads tile rows w and w + 8 whole (1 KB
+    //     each, row r at r·kStreamPitch), and every wave reads every row,
+    //     so each stage ends in a workgroup barrier.
+    //   * WPR (two or more x tiles): wave w loads only what it computes on,
+    //     its 64 k of all 16 rows, into its own 2 KB of the slot: group h
+    //     (tile rows 8h..8h+7) at byte 1024·h, lane l bringing row
+    //     8h + l/8's 16-byte piece (l % 8) ^ (row >> 1) to byte 16·l, so a
+    //     fragment read of 16 rows at one piece hits 16 distinct bank
+    //     slots.  A wave's slots are then its own: its vmcnt wait alone
+    //     makes a stage readable, and only the reduction needs barriers
+    //     (measured, bit-identical, two alternating runs: gate_up M = 32 /
+    //     48 / 64 22.1-22.2 -> 21.3, 24.6-24.7 -> 23.9, 26.3-26.5 -> 25.9-26.0
+    //     us, lm_head M = 32 120.9-121.6 -> 119.6-119.7 us; with one tile
+    //     the 8-row pieces ingest more slowly and the stage barrier costs
+    //     less, lm_head M = 5-16 1.3-2.2 us slower).
+    constexpr bool WPR = MT >= 2;
     const int klane = 8 * lane;
+    const int rho = lane >> 3, lj = lane & 7;
     auto issue = [&](int t) {
         const int bi = t / nst;
         const int st = sb + (t - bi * nst);
         const int b = vg + bi * Gs;
-        unsigned char* slot = ring + (size_t)(t % depth) * kStreamSlot;
-        const int k = st * kStreamKC + klane;
-        const int kc = k < K ? k : 0;  // past K: any in-range address, masked at use
+        unsigned char* slot = ring + (size_t)(t % depth) * kStreamSlot + (WPR ? wave * 2048 : 0);
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-            const int row = wave + WV * i;  // tile row 0..15
+            const int row = WPR ? 8 * i + rho : wave + WV * i;  // tile row 0..15
+            const int k = st * kStreamKC + (WPR ? 64 * wave + 8 * (lj ^ (row >> 1)) : klane);
+            const int kc = k < K ? k : 0;  // past K: any in-range address, masked at use
             int wr;
             if (SILU) {
                 int ch = b * CB + (row & 7);
@@ -159,7 +179,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 const int ch = b * CB + row;
                 wr = ch < Nout ? ch : Nout - 1;
             }
-            dma_row_stream(w + (int64_t)wr * ldw + kc, slot + row * kStreamPitch);
+            dma_row_stream(w + (int64_t)wr * ldw + kc, slot + (WPR ? i * 1024 : row * kStreamPitch));
         }
     };
     // x fragments X[j][kk][i] of the workgroup's K stages: lane (r, q) =
@@ -387,15 +407,23 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         for (int j = 0; j < XS; ++j) {
             if (j < nst) {
                 vm_wait_stages<LPW>(min(depth - 2, T - 1 - t));
-                bare_barrier();  // stage t landed for every wave; the slot of t-1 is free
+                // One tile: stage t landed for every wave and the slot of t - 1
+                // is free.  WPR: at a block's first stage the barrier
+                // publishes the last block's partial sums; with one
+                // reduction area, the second stage's barrier keeps this
+                // block's sums from being parked before every wave has
+                // read the last block's.
+                if (!WPR || j == 0 || (j == 1 && nred == 1)) bare_barrier();
                 if (t + depth - 1 < T) issue(t + depth - 1);
                 if (j == 0 && bi > 0) finish_block(bi - 1, (bi & 1) ? red0 : red1);
-                const unsigned char* slot = ring + (size_t)(t % depth) * kStreamSlot;
+                const unsigned char* slot = ring + (size_t)(t % depth) * kStreamSlot + (WPR ? wave * 2048 : 0);
                 const bool ktail = (sb + j + 1) * kStreamKC > K;
 #pragma unroll
                 for (int kk = 0; kk < KPW; ++kk) {
                     const int chunk = 4 * (wave * KPW + kk) + q;  // 16-byte chunk of the 1 KB row
-                    u32x4 v = *reinterpret_cast<const u32x4*>(slot + r * kStreamPitch + 16 * chunk);
+                    const int pc = 4 * kk + q;  // the piece within the wave's 64 k
+                    u32x4 v = *reinterpret_cast<const u32x4*>(
+                        slot + (WPR ? (r >> 3) * 1024 + (r & 7) * 128 + 16 * (pc ^ (r >> 1)) : r * kStreamPitch + 16 * chunk));
                     if (ktail) v &= ((sb + j) * kStreamKC + 8 * chunk < K) ? 0xffffffffu : 0u;
                     const bf16x8 bw = __builtin_bit_cast(bf16x8, v);
 #pragma unroll
@@ -407,9 +435,10 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             }
         }
 
-        // Park this block's partial sums; the next stage barrier publishes
-        // them.  Buffer bi % 2 was last read by the epilogue of block bi - 2,
-        // which ran before at least one barrier this wave has since passed.
+        // Park this block's partial sums; the next block's first barrier
+        // publishes them.  Buffer bi % 2 was last read by the epilogue of
+        // block bi - 2, which ran before at least one barrier this wave has
+        // since passed (with one area: this block's second-stage barrier).
         f32x4* const rb = (bi & 1) ? red1 : red0;
 #pragma unroll
         for (int i = 0; i < MT; ++i) rb[(wave * MT + i) * 64 + lane] = acc[i];
