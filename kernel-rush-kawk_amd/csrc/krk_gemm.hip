@@ -166,7 +166,12 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    // M = 17-32 (two x tiles): 4 ring slots, 0.2-0.3 us under 5 at M = 20,
+    // 24, 28 and 32 in three alternating passes once the stream kernel's
+    // multi-tile stages lost their workgroup barrier; 5 elsewhere.
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 16, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 32, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
     {2560, 9728, KRK_EPILOGUE_NONE, 1, 1, kcfg(KRK_KERNEL_VALU, 1, 0, 5, 1)},
     // M = 2-12: the wave-sliced kernel on 256 blocks of 10 channels, K
