@@ -358,7 +358,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
         constexpr int LS = SILU ? 8 : 16;    // channels of a 16-row tile with outputs
         constexpr int LSB = SILU ? 3 : 4;    // log2(LS)
         constexpr int ITEMS = MT * 4 * LS * 4;
-        for (int it = threadIdx.x; it < ITEMS; it += blockDim.x) {
+        auto item = [&](int it, int n) {  // n = it / 512, the thread's item slot
             const int e = it & 3;
             const int rr = (it >> 2) & (LS - 1);
             const int qq = (it >> (2 + LSB)) & 3;
@@ -386,13 +386,31 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                     // the blocks so far (reduced across channels at the end).
                     if (m < M && c < Nout) {
                         const uint64_t key = sel_key(v, (uint32_t)c);
-                        if constexpr (SK == 1) best[it / 512][0] = umax64(best[it / 512][0], key);
-                        else topk_insert(best[it / 512], key);
+                        if constexpr (SK == 1) best[n][0] = umax64(best[n][0], key);
+                        else topk_insert(best[n], key);
                     }
                 }
             } else if (m < M && c < Nout) {
                 o.put(m, c, g, u);
             }
+        };
+        if constexpr (ITEMS % 512 != 0) {
+            // Item counts that leave threads idle or give some two items
+            // (gate_up at 1-3 x tiles, lm_head at 1 or 3): the thread's items
+            // unrolled (512 threads), so the LDS reads of all of them go out
+            // before the first sum waits.  Measured, bit-identical: gate_up
+            // M = 9-16 / 32 / 48 0.6 / 0.35 / 1.1 us faster, lm_head plans at
+            // M = 5-16 3.5-4.3 us and M = 48 3.3 us faster.  Counts that are a
+            // multiple of 512 keep the loop: unrolled, lm_head at M = 24-32
+            // was 1.8-2.4 us slower, and at four x tiles the kernel spilled
+            // past 256 VGPRs (lm_head M = 64 18 us slower).
+#pragma unroll
+            for (int n = 0; n < (ITEMS + 511) / 512; ++n) {
+                const int it = threadIdx.x + 512 * n;
+                if (ITEMS % 512 == 0 || it < ITEMS) item(it, n);
+            }
+        } else {
+            for (int it = threadIdx.x; it < ITEMS; it += blockDim.x) item(it, it / 512);
         }
         if (splits > 1) splitk_finish<SILU, 1, 1>(o, ctr, b, b * CB, CB);
     };
