@@ -410,7 +410,7 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                 o.put(m, c, g, u);
             }
         };
-        if constexpr (ITEMS % 512 != 0) {
+        if constexpr (ITEMS % 512 != 0 || (SILU && MT == 4)) {
             // Item counts that leave threads idle or give some two items
             // (gate_up at 1-3 x tiles, lm_head at 1 or 3): the thread's items
             // unrolled (512 threads), so the LDS reads of all of them go out
@@ -418,8 +418,11 @@ stream_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
             // M = 9-16 / 32 / 48 0.6 / 0.35 / 1.1 us faster, lm_head plans at
             // M = 5-16 3.5-4.3 us and M = 48 3.3 us faster.  Counts that are a
             // multiple of 512 keep the loop: unrolled, lm_head at M = 24-32
-            // was 1.8-2.4 us slower, and at four x tiles the kernel spilled
-            // past 256 VGPRs (lm_head M = 64 18 us slower).
+            // was 1.8-2.4 us slower, and at four plain x tiles the kernel
+            // spilled past 256 VGPRs (lm_head M = 64 18 us slower).  The
+            // SwiGLU epilogue at four x tiles (512 items) is the exception:
+            // unrolled it fits (255 VGPRs) and gate_up at M = 49-64 measured
+            // 0.55-0.6 us faster (M = 64 24.66-24.69 -> 24.06-24.13 us).
 #pragma unroll
             for (int n = 0; n < (ITEMS + 511) / 512; ++n) {
                 const int it = threadIdx.x + 512 * n;
