@@ -165,11 +165,13 @@ const TableEntry kTable[] = {
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 1, 1, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 2, 2, kcfg(KRK_KERNEL_VALU, 2, 0, 2, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 3, 4, kcfg(KRK_KERNEL_VALU, 2, 0, 8, 1)},
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 8, kcfg(KRK_KERNEL_VALU, 4, 0, 4, 1)},
-    // M = 17-32 (two x tiles): 4 ring slots, 0.2-0.3 us under 5 at M = 20,
-    // 24, 28 and 32 in three alternating passes once the stream kernel's
-    // multi-tile stages lost their workgroup barrier; 5 elsewhere.
-    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 9, 16, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
+    // M = 5-16: the stream kernel, 5 ring slots (M = 5-8 18.7-19.1 us against
+    // 20.0-22.9 us for the VALU plan in three alternating passes, once the
+    // stream kernel's block epilogue batched its reads).  M = 17-32 (two x
+    // tiles): 4 ring slots, 0.2-0.3 us under 5 at M = 20, 24, 28 and 32 in
+    // three alternating passes once the stream kernel's multi-tile stages
+    // lost their workgroup barrier; 5 elsewhere.
+    {19456, 2560, KRK_EPILOGUE_SILU_MUL, 5, 16, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 17, 32, kcfg(KRK_KERNEL_STREAM, 1, 4, 0, 1)},
     {19456, 2560, KRK_EPILOGUE_SILU_MUL, 33, 64, kcfg(KRK_KERNEL_STREAM, 1, 5, 0, 1)},
     // down 9728 -> 2560
